@@ -1,0 +1,219 @@
+#!/usr/bin/env python
+"""Encoder throughput on one MI355X: encoded 16x16 tiles/s and the fraction of
+the packed-fp16 VALU roofline, with the CPU oracle timed beside it.
+
+Workload: one 1024x1024 matrix of i.i.d. N(0,1)
+fp16 values (seed 1), cut into 4096 16x16 tiles as the LDLQ loop forms them
+(16-row blocks, tensor-core permutation), encoded at K=4 with the MUL1
+codebook; K=2 is measured on the same matrix and reported beside it.
+Synthetic data, inputs resident in HBM before the timed region. One step =
+the full device-side encode of the batch: pass-1 forward, traceback, pass-2
+forward, traceback (exl3_quantize_tiles) plus the finalize kernel (packing,
+path cost, distortion). ``--sweep`` adds K=2..6 on the 4096x4096
+heavy-tailed matrix of configs[2] (65536 tiles).
+
+Roofline: algorithmic work per forward-pass launch = tiles * 256 steps *
+65536 candidates * 3 fp16 element-ops (subtract, FMA, compare-select);
+``achieved`` divides it by the forward kernel's mean duration measured with
+HIP events on the stream the kernel runs on. Peak = 256 CU * 64 lanes * 2
+(packed fp16) * 2.4 GHz = 78.64 T fp16 element-ops/s (the published
+157.3 TFLOP/s fp16 vector rate counts each FMA twice).
+
+    python bench.py [--steps 10] [--warmup 2] [--sweep] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = ("encoded 16x16 tiles/sec at K=2 and K=4, 1 MI355X; % of fp16 VALU/LDS roofline")
+PEAK_ELEM_OPS = 256 * 64 * 2 * 2.4e9          # fp16 element-ops/s
+OPS_PER_TILE_PASS = 256 * 65536 * 3            # one forward pass
+
+
+def config2_tiles() -> np.ndarray:
+    rng = np.random.default_rng(1)
+    W = rng.standard_normal((1024, 1024), dtype=np.float32).astype(np.float16).astype(np.float32)
+    return W.reshape(64, 16, 64, 16).transpose(0, 2, 1, 3).reshape(4096, 256)
+
+
+def config3_tiles() -> np.ndarray:
+    rng = np.random.default_rng(2)
+    W = rng.standard_normal((4096, 4096), dtype=np.float32)
+    W = np.where(rng.random(W.shape) < 0.01, 4.0 * W, W)
+    W = W.astype(np.float16).astype(np.float32)
+    return W.reshape(256, 16, 256, 16).transpose(0, 2, 1, 3).reshape(65536, 256)
+
+
+class DeviceBatch:
+    """A batch prepared on the device with its scratch, ready to encode."""
+
+    def __init__(self, raw_np, K, torch, ext, batch_cap=None):
+        from exl3_intel_arc_quantizer_amd._native import row_bytes
+        self.torch, self.ext, self.K = torch, ext, K
+        self.n = raw_np.shape[0]
+        self.raw = torch.from_numpy(raw_np).cuda()
+        self.x = torch.empty_like(self.raw)
+        ext.prepare_tiles(self.raw, self.x, True)
+        cap = batch_cap or self.n
+        self.cap = cap
+        self.costs = torch.empty((cap, 2, 65536 >> K), dtype=torch.float16, device="cuda")
+        self.edges = torch.empty((cap, 257, row_bytes(K)), dtype=torch.uint8, device="cuda")
+        self.out_w = torch.empty((self.n, 256), dtype=torch.float32, device="cuda")
+        self.out_i = torch.empty((self.n, 256), dtype=torch.int16, device="cuda")
+        self.packed = torch.empty((self.n, 16 * K), dtype=torch.int16, device="cuda")
+        self.pc = torch.empty(self.n, dtype=torch.float32, device="cuda")
+        self.dist = torch.empty(self.n, dtype=torch.float32, device="cuda")
+        self.rec = torch.empty((self.n, 256), dtype=torch.int16, device="cuda")
+        self.pre = torch.full((cap,), -1, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+
+    def step(self):
+        self.ext.quantize_tiles(self.x, self.out_w, self.out_i, self.costs, self.edges, self.K,
+                                False, True)
+        self.ext.finalize_tiles(self.x, self.raw, self.out_w, self.out_i, self.packed, self.pc,
+                                self.dist, self.rec, self.K, True)
+
+    def forward_only(self, n):
+        self.ext.quantize_tiles_forward_pass(self.x[:n], self.costs[:n], self.edges[:n],
+                                             self.pre[:n], self.K, False, True, 0, 1)
+
+
+def time_steps(batch, steps, warmup, torch):
+    for _ in range(warmup):
+        batch.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        batch.step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def forward_kernel_roofline(batch, torch, reps=3):
+    """Mean duration of one forward-pass launch over the whole batch, timed
+    with HIP events recorded on the launch stream."""
+    n = min(batch.n, batch.cap)
+    batch.forward_only(n)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        batch.forward_only(n)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    ops = n * OPS_PER_TILE_PASS
+    achieved = ops / (ms * 1e-3)
+    return {"bound": "valu", "achieved": round(achieved / 1e12, 3),
+            "peak": round(PEAK_ELEM_OPS / 1e12, 3), "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_ELEM_OPS, 4), "traffic": None,
+            "kernel": f"acs_forward_fast<K={batch.K}>", "launch_ms": round(ms, 3),
+            "tiles_per_launch": n,
+            "ops_note": "fp16 element-ops: tiles*256 steps*65536 candidates*3 (sub, FMA, "
+                        "compare-select); peak 256 CU*64 lanes*2 halves*2.4 GHz"}
+
+
+def cpu_baseline(tiles, K):
+    """The C oracle (oracle/libexl3_oracle.so, a port of the reference's CPU
+    encoder) on a bounded sample of the same workload, all host cores."""
+    from oracle import c_oracle
+    cores = c_oracle.default_threads()
+    n = max(cores, 2 * cores)
+    sample = tiles[:n]
+    c_oracle.encode_tiles(sample[:1], K=K, cb=2, pre_permute=True, threads=1)  # load + warm
+    t0 = time.perf_counter()
+    c_oracle.encode_tiles(sample, K=K, cb=2, pre_permute=True, threads=cores)
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 3), "unit": "tiles/s", "cores": cores, "kind": "port",
+            "sample": f"first {n} tiles of the benchmark matrix at K={K} "
+                      f"({dt:.1f} s, C restatement of reference_encoder.py, OpenMP)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--sweep", action="store_true", help="also run K=2..6 on configs[2]")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the encoder "
+              "shards by tiles across GPUs, see DESIGN.md", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from exl3_intel_arc_quantizer_amd.gpu_quantizer import build_quantize_extension
+    ext = build_quantize_extension()
+    tiles = config2_tiles()
+
+    results = {}
+    for K in (4, 2):
+        b = DeviceBatch(tiles, K, torch, ext)
+        sec = time_steps(b, args.steps, args.warmup, torch)
+        results[K] = {"tiles_per_s": b.n / sec, "ms_per_step": sec * 1e3,
+                      "roofline": forward_kernel_roofline(b, torch)}
+        print(f"# K={K}: {b.n / sec:,.0f} tiles/s, {sec * 1e3:.2f} ms/step, forward "
+              f"{results[K]['roofline']['launch_ms']} ms = "
+              f"{100 * results[K]['roofline']['frac']:.1f}% of VALU peak", file=sys.stderr,
+              flush=True)
+        del b
+        torch.cuda.empty_cache()
+
+    sweep = None
+    if args.sweep:
+        sweep = {}
+        big = config3_tiles()
+        for K in (2, 3, 4, 5, 6):
+            b = DeviceBatch(big, K, torch, ext, batch_cap=8192)
+            sec = time_steps(b, max(1, args.steps // 5), 1, torch)
+            rf = forward_kernel_roofline(b, torch, reps=1)
+            sweep[K] = {"tiles_per_s": round(big.shape[0] / sec, 1),
+                        "valu_frac": rf["frac"], "forward_ms_8192_tiles": rf["launch_ms"]}
+            print(f"# sweep K={K}: {big.shape[0] / sec:,.0f} tiles/s, VALU {100 * rf['frac']:.1f}%",
+                  file=sys.stderr, flush=True)
+            del b
+            torch.cuda.empty_cache()
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(tiles, 4)
+    main_k = results[4]
+    line = {
+        "metric": METRIC,
+        "value": round(main_k["tiles_per_s"], 1),
+        "unit": "tiles/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_k["ms_per_step"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: 1024x1024 N(0,1) fp16 matrix (seed 1), 4096 tiles "
+                               "in LDLQ order, K=4, MUL1, L=256",
+                   "tiles": 4096, "K": 4, "codebook": "mul1"},
+        "roofline": main_k["roofline"],
+        "cpu_baseline": cpu,
+        "k2": {"value": round(results[2]["tiles_per_s"], 1), "unit": "tiles/s",
+               "ms_per_step": round(results[2]["ms_per_step"], 3),
+               "roofline": results[2]["roofline"]},
+    }
+    if sweep is not None:
+        line["sweep_configs2"] = sweep
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

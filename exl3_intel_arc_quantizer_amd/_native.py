@@ -1,0 +1,321 @@
+"""ctypes binding of ``libexl3_hip.so`` and the extension facade.
+
+``QuantizeExtension`` mirrors the functions of the reference's pybind module
+``quantize_xpu_ext`` (csrc/quantize_xpu/quantize_xpu.cpp:302-357) with the
+same names, argument order, defaults and error behaviour (``RuntimeError``
+for rejected tensors, as its ``TORCH_CHECK``s raise), but takes torch-ROCm
+device tensors (``cuda:i``) and calls the C-ABI declared in
+``include/exl3_encoder.h``. Work is enqueued on the tensor's current torch
+stream; nothing here synchronises.
+
+There is no CPU fallback: loading fails loudly when the library is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+from .build import LIB_PATH
+
+_LIB = None
+
+_c_int, _c_i64, _c_vp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "exl3_last_error": (ctypes.c_char_p, []),
+    "exl3_version": (ctypes.c_char_p, []),
+    "exl3_decode_codebook": (_c_int, [_c_int, _c_vp, _c_vp]),
+    "exl3_scratch_row_bytes": (_c_i64, [_c_int]),
+    "exl3_scratch_edges_bytes": (_c_i64, [_c_int, _c_int, _c_i64]),
+    "exl3_backpointer_slot": (_c_i64, [_c_int, _c_i64]),
+    "exl3_quantize_tiles": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int,
+                                     _c_int, _c_int, _c_int, _c_i64, _c_vp]),
+    "exl3_forward_pass": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
+                                   _c_int, _c_int, _c_int, _c_vp]),
+    "exl3_backward_pass": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_int,
+                                    _c_int, _c_int, _c_int, _c_int, _c_vp]),
+    "exl3_prepare_tiles": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
+    "exl3_finalize_tiles": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                     _c_i64, _c_int, _c_int, _c_int, _c_vp]),
+    "exl3_pack_trellis": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
+    "exl3_probe_hfma": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
+}
+
+
+def exported_symbols() -> list:
+    """C-ABI entry points declared in include/exl3_encoder.h."""
+    return sorted(_SIGNATURES)
+
+
+def load_library(path: Optional[Path] = None):
+    """Load the native library (no build, no fallback)."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    lib_path = Path(path) if path is not None else LIB_PATH
+    if not lib_path.exists():
+        raise RuntimeError(
+            f"native encoder library {lib_path} is missing; build it with "
+            "`python -m exl3_intel_arc_quantizer_amd.build` (hipcc, gfx950)")
+    lib = ctypes.CDLL(str(lib_path))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def last_error() -> str:
+    return load_library().exl3_last_error().decode()
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what}: {last_error()}")
+
+
+# ------------------------------------------------------------- validation
+
+def _torch():
+    import torch
+    return torch
+
+
+def _check_device_tensor(t, name: str, dtype, ndim: int) -> int:
+    """TORCH_CHECK equivalents of check_xpu_tensor (quantize_xpu.cpp:73-83)."""
+    torch = _torch()
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a GPU (cuda) tensor")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} has wrong dtype")
+    if t.dim() != ndim:
+        raise RuntimeError(f"{name} must be {ndim}-D, got {t.dim()}-D")
+    return t.device.index if t.device.index is not None else torch.cuda.current_device()
+
+
+def _resolve_cb(mcg: bool, mul1: bool) -> int:
+    """quantize_xpu.cpp:85-91."""
+    if mcg and mul1:
+        raise RuntimeError("mcg and mul1 cannot both be true (ambiguous codebook)")
+    return 2 if mul1 else (1 if mcg else 0)
+
+
+def _validate_common(K: int, cb: int, L: int, sg_size: int) -> None:
+    """quantize_xpu.cpp:93-101. sg_size is accepted for API parity; wave64
+    hardware has no sub-group width choice."""
+    if not 1 <= K <= 8:
+        raise RuntimeError(f"K must be in 1..8, got {K}")
+    if L not in (256, 160):
+        raise RuntimeError(f"tile length L must be 256 or 160, got {L}")
+    if L == 160 and cb != 2:
+        raise RuntimeError("tile length L=160 is only supported with mul1 (cb=2)")
+    if sg_size not in (16, 32):
+        raise RuntimeError(f"sg_size must be 16 or 32, got {sg_size}")
+
+
+def _stream(device_index: int) -> int:
+    torch = _torch()
+    return torch.cuda.current_stream(device_index).cuda_stream
+
+
+def row_bytes(K: int) -> int:
+    return int(load_library().exl3_scratch_row_bytes(K))
+
+
+class QuantizeExtension:
+    """Drop-in for the reference's ``quantize_xpu_ext`` module object."""
+
+    def __init__(self, lib=None):
+        self.lib = lib or load_library()
+
+    # quantize_xpu.cpp:105-110
+    def decode_codebook(self, cb: int, out_lut) -> None:
+        torch = _torch()
+        if not 0 <= cb <= 2:
+            raise RuntimeError("cb must be 0, 1, or 2")
+        dev = _check_device_tensor(out_lut, "out_lut", torch.float16, 1)
+        if out_lut.size(0) != 65536:
+            raise RuntimeError("out_lut must have length 65536")
+        with torch.cuda.device(dev):
+            _check(self.lib.exl3_decode_codebook(cb, out_lut.data_ptr(), _stream(dev)),
+                   "decode_codebook")
+
+    def _scratch_checks(self, temp_costs, temp_edges, K: int, L: int, dev: int) -> int:
+        torch = _torch()
+        if _check_device_tensor(temp_costs, "temp_costs", torch.float16, 3) != dev:
+            raise RuntimeError("temp_costs must be on the same GPU device as input_tiles")
+        if _check_device_tensor(temp_edges, "temp_edges", torch.uint8, 3) != dev:
+            raise RuntimeError("temp_edges must be on the same GPU device as input_tiles")
+        edges = 65536 >> K
+        batch_cap = temp_costs.size(0)
+        if batch_cap < 1:
+            raise RuntimeError("temp_costs batch dimension B must be >= 1")
+        if temp_costs.size(1) != 2 or temp_costs.size(2) != edges:
+            raise RuntimeError("temp_costs must have shape (B, 2, 65536 >> K)")
+        rb = row_bytes(K)
+        if (temp_edges.size(0) < batch_cap or temp_edges.size(1) != L + 1
+                or temp_edges.size(2) != rb):
+            raise RuntimeError(
+                f"temp_edges must have shape (B, L + 1, {rb}) for K={K} (K-bit backpointer layout)")
+        return batch_cap
+
+    # quantize_xpu.cpp:112-167
+    def quantize_tiles(self, input_tiles, output_tiles, output_indices, temp_costs, temp_edges,
+                       K: int, mcg: bool, mul1: bool, sg_size: int = 32,
+                       force_global_costs: bool = False, wave_cap_override: int = 0) -> None:
+        torch = _torch()
+        cb = _resolve_cb(mcg, mul1)
+        dev = _check_device_tensor(input_tiles, "input_tiles", torch.float32, 2)
+        if _check_device_tensor(output_tiles, "output_tiles", torch.float32, 2) != dev:
+            raise RuntimeError("output_tiles must be on the same GPU device as input_tiles")
+        if _check_device_tensor(output_indices, "output_indices", torch.int16, 2) != dev:
+            raise RuntimeError("output_indices must be on the same GPU device as input_tiles")
+        n, L = input_tiles.shape
+        if n <= 0:
+            raise RuntimeError(f"num_tiles must be positive, got {n}")
+        _validate_common(K, cb, L, sg_size)
+        batch_cap = self._scratch_checks(temp_costs, temp_edges, K, L, dev)
+        if tuple(output_tiles.shape) != (n, L):
+            raise RuntimeError("output_tiles shape must match input_tiles")
+        if tuple(output_indices.shape) != (n, L):
+            raise RuntimeError("output_indices shape must match input_tiles")
+        with torch.cuda.device(dev):
+            _check(self.lib.exl3_quantize_tiles(
+                input_tiles.data_ptr(), output_tiles.data_ptr(), output_indices.data_ptr(),
+                temp_costs.data_ptr(), temp_edges.data_ptr(), batch_cap, n, K, cb, L,
+                int(bool(force_global_costs)), int(wave_cap_override), _stream(dev)),
+                "quantize_tiles")
+
+    # quantize_xpu.cpp:169-215
+    def quantize_tiles_forward_pass(self, input_tiles, temp_costs, temp_edges, pre_states,
+                                    K: int, mcg: bool, mul1: bool, roll: int, cost_slot: int = 0,
+                                    sg_size: int = 32, force_global_costs: bool = False) -> None:
+        torch = _torch()
+        cb = _resolve_cb(mcg, mul1)
+        dev = _check_device_tensor(input_tiles, "input_tiles", torch.float32, 2)
+        if _check_device_tensor(pre_states, "pre_states", torch.int32, 1) != dev:
+            raise RuntimeError("pre_states must be an int32 GPU tensor")
+        n, L = input_tiles.shape
+        _validate_common(K, cb, L, sg_size)
+        batch_cap = self._scratch_checks(temp_costs, temp_edges, K, L, dev)
+        if not 0 < n <= batch_cap:
+            raise RuntimeError("num_tiles must be in 1..B")
+        if pre_states.size(0) < n:
+            raise RuntimeError("pre_states length must be >= num_tiles")
+        if cost_slot not in (0, 1):
+            raise RuntimeError("cost_slot must be 0 or 1")
+        with torch.cuda.device(dev):
+            _check(self.lib.exl3_forward_pass(
+                input_tiles.data_ptr(), temp_costs.data_ptr(), temp_edges.data_ptr(),
+                pre_states.data_ptr(), n, K, cb, L, int(roll), int(cost_slot),
+                int(bool(force_global_costs)), _stream(dev)), "quantize_tiles_forward_pass")
+
+    # quantize_xpu.cpp:217-259
+    def quantize_tiles_backward_pass(self, temp_costs, temp_edges, output_tiles, output_indices,
+                                     end_states, num_tiles: int, K: int, mcg: bool, mul1: bool,
+                                     roll: int, cost_slot: int, write_output: bool,
+                                     sg_size: int = 32) -> None:
+        torch = _torch()
+        cb = _resolve_cb(mcg, mul1)
+        dev = _check_device_tensor(temp_costs, "temp_costs", torch.float16, 3)
+        if _check_device_tensor(output_tiles, "output_tiles", torch.float32, 2) != dev:
+            raise RuntimeError("output_tiles must be on the same GPU device")
+        if _check_device_tensor(output_indices, "output_indices", torch.int16, 2) != dev:
+            raise RuntimeError("output_indices must be on the same GPU device")
+        if _check_device_tensor(end_states, "end_states", torch.int32, 1) != dev:
+            raise RuntimeError("end_states must be an int32 GPU tensor")
+        L = temp_edges.size(1) - 1
+        _validate_common(K, cb, L, sg_size)
+        batch_cap = self._scratch_checks(temp_costs, temp_edges, K, L, dev)
+        if not 0 < num_tiles <= batch_cap:
+            raise RuntimeError("num_tiles must be in 1..B")
+        if end_states.size(0) < num_tiles:
+            raise RuntimeError("end_states length must be >= num_tiles")
+        if write_output and (output_tiles.size(0) < num_tiles or output_tiles.size(1) != L
+                             or output_indices.size(0) < num_tiles
+                             or output_indices.size(1) != L):
+            raise RuntimeError("output tensors must have shape (>= num_tiles, L)")
+        with torch.cuda.device(dev):
+            _check(self.lib.exl3_backward_pass(
+                temp_costs.data_ptr(), temp_edges.data_ptr(), output_tiles.data_ptr(),
+                output_indices.data_ptr(), end_states.data_ptr(), int(num_tiles), K, cb, L,
+                int(roll), int(cost_slot), int(bool(write_output)), _stream(dev)),
+                "quantize_tiles_backward_pass")
+
+    # -------------------------------------------------- device-side helpers
+
+    def prepare_tiles(self, raw, out, permute: bool) -> None:
+        torch = _torch()
+        dev = _check_device_tensor(raw, "raw", torch.float32, 2)
+        _check_device_tensor(out, "out", torch.float32, 2)
+        n, L = raw.shape
+        if tuple(out.shape) != (n, L):
+            raise RuntimeError("out must match raw")
+        with torch.cuda.device(dev):
+            _check(self.lib.exl3_prepare_tiles(raw.data_ptr(), out.data_ptr(), n, L,
+                                               int(bool(permute)), _stream(dev)), "prepare_tiles")
+
+    def finalize_tiles(self, x, raw, out_w, out_idx, packed, path_cost, distortion, recon_orig,
+                       K: int, permuted: bool) -> None:
+        torch = _torch()
+        dev = _check_device_tensor(x, "x", torch.float32, 2)
+        n, L = x.shape
+        for t, name, dt, nd in ((out_w, "out_w", torch.float32, 2),
+                                (out_idx, "out_idx", torch.int16, 2),
+                                (path_cost, "path_cost", torch.float32, 1),
+                                (distortion, "distortion", torch.float32, 1),
+                                (recon_orig, "recon_orig", torch.int16, 2)):
+            if _check_device_tensor(t, name, dt, nd) != dev:
+                raise RuntimeError(f"{name} must be on the same GPU device")
+        if packed is not None:
+            _check_device_tensor(packed, "packed", torch.int16, 2)
+            if tuple(packed.shape) != (n, 16 * K):
+                raise RuntimeError("packed must have shape (n, 16*K)")
+        if permuted:
+            _check_device_tensor(raw, "raw", torch.float32, 2)
+        with torch.cuda.device(dev):
+            _check(self.lib.exl3_finalize_tiles(
+                x.data_ptr(), raw.data_ptr() if permuted else None, out_w.data_ptr(),
+                out_idx.data_ptr(), packed.data_ptr() if packed is not None else None,
+                path_cost.data_ptr(), distortion.data_ptr(), recon_orig.data_ptr(), n, K, L,
+                int(bool(permuted)), _stream(dev)), "finalize_tiles")
+
+    def pack_trellis(self, states, packed, K: int) -> None:
+        torch = _torch()
+        dev = _check_device_tensor(states, "states", torch.int16, 2)
+        _check_device_tensor(packed, "packed", torch.int16, 2)
+        n = states.size(0)
+        if states.size(1) != 256 or tuple(packed.shape) != (n, 16 * K):
+            raise RuntimeError("pack_trellis expects (n, 256) states and (n, 16*K) words")
+        with torch.cuda.device(dev):
+            _check(self.lib.exl3_pack_trellis(states.data_ptr(), packed.data_ptr(), n, K,
+                                              _stream(dev)), "pack_trellis")
+
+    def probe_hfma(self, dh, cost, out, mode: int) -> None:
+        """exl3_quant/xpu_probe.py ``probe_hfma`` (mode 0: fused, 1: two roundings)."""
+        torch = _torch()
+        dev = _check_device_tensor(dh, "dh", torch.float16, 1)
+        _check_device_tensor(cost, "cost", torch.float16, 1)
+        _check_device_tensor(out, "out", torch.float16, 1)
+        with torch.cuda.device(dev):
+            _check(self.lib.exl3_probe_hfma(dh.data_ptr(), cost.data_ptr(), out.data_ptr(),
+                                            dh.numel(), int(mode), _stream(dev)), "probe_hfma")
+
+
+_EXT: Optional[QuantizeExtension] = None
+
+
+def extension() -> QuantizeExtension:
+    global _EXT
+    if _EXT is None:
+        _EXT = QuantizeExtension()
+    return _EXT

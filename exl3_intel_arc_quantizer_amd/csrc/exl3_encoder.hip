@@ -1,0 +1,798 @@
+// MI355X (gfx950) EXL3 trellis tile encoder: HIP kernels + C-ABI.
+//
+// Path: the two-pass tail-biting Viterbi search of the reference's
+// ReferenceTrellisEncoder.encode_tile (exl3_quant/reference_encoder.py:253-324)
+// and its SYCL kernel FusedQuantizeKernel (quantize_kernels.sycl:245-360),
+// re-designed for CDNA4:
+//
+//   acs_forward_fast   one 1024-thread workgroup per tile; fp16 path costs
+//                      ping-pong in LDS; each thread owns 64 (edge, branch)
+//                      candidates whose codebook values live in 32 VGPRs for
+//                      the whole launch; packed-fp16 subtract/FMA; the
+//                      first-minimum over branches is an unsigned min over
+//                      32-bit keys (cost bits << 16 | branch); winning branches
+//                      leave as K-bit backpointers in coalesced 16/32-bit
+//                      stores, only for the ring rows the traceback reads.
+//   acs_forward_generic reference-structured kernel (one edge per thread
+//                      iteration, codebook decoded per candidate, strict fp16
+//                      '<' scan): K = 8 and the force_global_costs variant.
+//   traceback_kernel   one lane per tile walks the K-bit backpointers.
+//   finalize_kernel    packing, path cost, distortion, un-permutation.
+//
+// Numerics (bit-exact vs the reference on finite / infinite inputs):
+//   dh = fp16(val - w) (v_pk_add_f16), err = fma_f16(dh, dh, cost_prev)
+//   (v_pk_fma_f16, one rounding, fp16 denormals preserved). Step 0 is the
+//   same FMA against an initial cost vector of +0 (unconstrained) or
+//   {+0 at pre_state, +inf elsewhere}: fma(dh, dh, +0) == fp16(dh*dh) and
+//   fma(dh, dh, +inf) == +inf, which is the reference's masked step 0
+//   (reference_encoder.py:152-179).
+//   Costs are non-negative fp16 or +inf, whose bit patterns order like their
+//   values, so min over (cost_bits << 16 | k) picks the lowest k among equal
+//   minima — the reference's "k = 0 initialises, later k replaces only if
+//   strictly smaller" rule (reference_encoder.py:169-176,193-199). NaN inputs
+//   are rejected by the host wrapper (see the package's encoder module).
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+
+#include "../../include/exl3_encoder.h"
+#include "exl3_layout.h"
+
+using exl3::BpLayout;
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+#define EXL3_VERSION "exl3-mi355x 0.1.0"
+
+// ------------------------------------------------------------------ errors
+
+static thread_local std::string g_last_error;
+
+static int set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+static int set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return 1;
+}
+
+static int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+  return 0;
+}
+
+// --------------------------------------------------------------- codebook
+
+__device__ __forceinline__ f16 f16_bits(uint32_t b) {
+  return __builtin_bit_cast(f16, (uint16_t)b);
+}
+__device__ __forceinline__ uint16_t bits_f16(f16 h) { return __builtin_bit_cast(uint16_t, h); }
+
+// fp16 value of state s (reference trellis_format.py:41-81,
+// quantize_kernels.sycl:51-73; upstream codebook.cuh:56-123).
+__device__ __forceinline__ f16 decode_state(int cb, uint32_t s) {
+  if (cb == 2) {
+    const uint32_t x = s * 0x83DCD12Du;
+    const uint32_t bsum = (x & 0xFFu) + ((x >> 8) & 0xFFu) + ((x >> 16) & 0xFFu) + (x >> 24);
+    // 0x6400 + bsum is the fp16 encoding of 1024 + bsum; one fused fp16 FMA.
+    return __builtin_fmaf16(f16_bits(0x6400u + bsum), f16_bits(0x1EEEu), f16_bits(0xC931u));
+  }
+  uint32_t x = (cb == 0) ? (s * 89226354u + 64248484u) : (s * 0xCBAC1FEDu);
+  x = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+  return f16_bits(x & 0xFFFFu) + f16_bits(x >> 16);
+}
+
+__global__ void decode_codebook_kernel(int cb, uint16_t* __restrict__ out) {
+  const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s < 65536u) out[s] = bits_f16(decode_state(cb, s));
+}
+
+// ------------------------------------------------------- tile permutation
+
+// tensor_core_perm (reference trellis_format.py:88-108): encoded element
+// 8t + s is original position row*16 + col with row in
+// {2(t%4), 2(t%4)+1, 2(t%4)+8, 2(t%4)+9}[s%4] and col = t/4 + 8*(s/4).
+__device__ __forceinline__ int tc_perm(int i) {
+  const int t = i >> 3, s = i & 7;
+  const int r0 = (t & 3) * 2;
+  const int row = r0 + (s & 1) + ((s >> 1) & 1) * 8;
+  const int col = (t >> 2) + (s >> 2) * 8;
+  return row * 16 + col;
+}
+
+// Inverse of tc_perm: original position p -> encoded element.
+__device__ __forceinline__ int tc_perm_inv(int p) {
+  const int row = p >> 4, col = p & 15;
+  const int t = ((col & 7) << 2) | ((row & 7) >> 1);
+  const int s = (row & 1) | ((row >> 3) << 1) | ((col >> 3) << 2);
+  return (t << 3) | s;
+}
+
+// ------------------------------------------------------- shared helpers
+
+__device__ __forceinline__ uint32_t umin(uint32_t a, uint32_t b) { return a < b ? a : b; }
+
+__device__ __forceinline__ uint32_t wave_min(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = umin(v, (uint32_t)__shfl_xor((int)v, m, 64));
+  return v;
+}
+
+// Lowest-index minimum of the terminal costs (reference argmin_cost,
+// reference_encoder.py:206-214): key = cost_bits << 16 | edge; all +inf
+// gives edge 0. Result broadcast to all threads via s_red[0].
+template <int NT>
+__device__ uint32_t block_argmin(const uint16_t* cost, int E, uint32_t* s_red) {
+  uint32_t best = 0xFFFFFFFFu;
+  for (int e = threadIdx.x; e < E; e += NT) best = umin(best, ((uint32_t)cost[e] << 16) | (uint32_t)e);
+  best = wave_min(best);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) s_red[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t b = s_red[0];
+    for (int w = 1; w < NT / 64; ++w) b = umin(b, s_red[w]);
+    s_red[0] = b;
+  }
+  __syncthreads();
+  return s_red[0] & 0xFFFFu;
+}
+
+// Arguments shared by both forward kernels. Tile t of the launch reads
+// in + t*L and owns scratch slot t.
+struct FwdArgs {
+  const float* in;
+  int n, L, roll, store_rows, cb;
+  const int32_t* pre_states;  // may be NULL: unconstrained
+  int64_t pre_stride;         // in int32 elements
+  uint8_t* bp;                // backpointer scratch, tile stride bp_tile_stride
+  int64_t bp_tile_stride;
+  uint16_t* term_costs;       // [slot][2][E] or NULL
+  int cost_slot;
+  int32_t* best_edges;        // terminal argmin per tile or NULL
+  int64_t best_stride;
+};
+
+// ------------------------------------------------------------ fast kernel
+
+template <int K, int G, int J, int P>
+struct FastCfg {
+  static constexpr int E = 65536 >> K;
+  static constexpr int S = 65536 >> (2 * K);  // groups
+  static constexpr int NB = 1 << K;           // branches
+  static constexpr int Q = NB / P;            // branches per lane
+  static constexpr int NJ = NB / J;           // edge sets per group set
+  static constexpr int NGQ = S / G;           // group sets
+  static constexpr int NT = NGQ * NJ * P;     // threads per tile
+  static constexpr int KR = 16 - K;
+  static constexpr int BPB = (K == 3) ? 4 : (K >= 5 ? 8 : K);
+  static constexpr int UNIT_BITS = G * J * BPB;
+  static constexpr int ROWB = E * BPB / 8;
+  static_assert(NT == 1024, "fast configurations use 1024 threads");
+  static_assert(G % 2 == 0, "groups are processed in packed pairs");
+  static_assert(UNIT_BITS == 16 || UNIT_BITS == 32, "unit store width");
+  static_assert(P == 1 || P == 2 || P == 4, "branch split within a quad");
+};
+
+template <int P>
+__device__ __forceinline__ uint32_t quad_min(uint32_t v) {
+  if (P >= 2) v = umin(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  if (P >= 4) v = umin(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  return v;
+}
+
+template <int K, int G, int J, int P>
+__global__ void __launch_bounds__(1024) acs_forward_fast(FwdArgs a) {
+  using C = FastCfg<K, G, J, P>;
+  __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][C::E];
+  __shared__ f16 s_w[256];
+  __shared__ uint32_t s_red[16];
+
+  const int tile = blockIdx.x;
+  const int L = a.L;
+  const int tid = threadIdx.x;
+  const int p = tid % P;
+  const int unit = tid / P;
+  const int jj = unit % C::NJ;
+  const int gq = unit / C::NJ;
+  const int h0 = gq * G;
+
+  // Codebook values of this thread's candidates: pair (g2, jl, q) holds the
+  // states of groups h0+2*g2 (low half) and h0+2*g2+1 (high half), edge
+  // j = jj*J + jl, branch k = p*Q + q.
+  f16x2 cbv[G / 2][J][C::Q];
+#pragma unroll
+  for (int g2 = 0; g2 < G / 2; ++g2)
+#pragma unroll
+    for (int jl = 0; jl < J; ++jl)
+#pragma unroll
+      for (int q = 0; q < C::Q; ++q) {
+        const uint32_t k = (uint32_t)(p * C::Q + q);
+        const uint32_t j = (uint32_t)(jj * J + jl);
+        const uint32_t s_lo = (k << C::KR) | ((uint32_t)(h0 + 2 * g2) << K) | j;
+        f16x2 v;
+        v.x = decode_state(a.cb, s_lo);
+        v.y = decode_state(a.cb, s_lo + (1u << K));
+        cbv[g2][jl][q] = v;
+      }
+
+  const float* in = a.in + (int64_t)tile * L;
+  for (int r = tid; r < L; r += C::NT) s_w[r] = (f16)in[r];
+  const int pre = a.pre_states ? a.pre_states[(int64_t)tile * a.pre_stride] : -1;
+  for (int e = tid; e < C::E; e += C::NT) s_cost[0][e] = (pre < 0 || e == pre) ? 0 : 0x7C00;
+  __syncthreads();
+
+  uint8_t* tile_bp = a.bp + (int64_t)tile * a.bp_tile_stride;
+
+  for (int i = 0; i < L; ++i) {
+    int ri = i + a.roll;
+    if (ri >= L) ri -= L;
+    const uint16_t* cin = s_cost[i & 1];
+    uint16_t* cout = s_cost[(i & 1) ^ 1];
+    const f16 w = s_w[ri];
+    f16x2 w2;
+    w2.x = w;
+    w2.y = w;
+
+    uint32_t best[G / 2][J][2];
+#pragma unroll
+    for (int g2 = 0; g2 < G / 2; ++g2)
+#pragma unroll
+      for (int jl = 0; jl < J; ++jl) best[g2][jl][0] = best[g2][jl][1] = 0xFFFFFFFFu;
+
+#pragma unroll
+    for (int q = 0; q < C::Q; ++q) {
+      const uint32_t k = (uint32_t)(p * C::Q + q);
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(cin + k * C::S + h0);
+      uint32_t cpair[G / 2];
+#pragma unroll
+      for (int g2 = 0; g2 < G / 2; ++g2) cpair[g2] = src[g2];
+#pragma unroll
+      for (int g2 = 0; g2 < G / 2; ++g2)
+#pragma unroll
+        for (int jl = 0; jl < J; ++jl) {
+          const f16x2 dh = cbv[g2][jl][q] - w2;
+          const f16x2 err =
+              __builtin_elementwise_fma(dh, dh, __builtin_bit_cast(f16x2, cpair[g2]));
+          const uint32_t eb = __builtin_bit_cast(uint32_t, err);
+          best[g2][jl][0] = umin(best[g2][jl][0], (eb << 16) | k);
+          best[g2][jl][1] = umin(best[g2][jl][1], (eb & 0xFFFF0000u) | k);
+        }
+    }
+
+    uint32_t bits = 0;
+#pragma unroll
+    for (int g2 = 0; g2 < G / 2; ++g2)
+#pragma unroll
+      for (int jl = 0; jl < J; ++jl)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const uint32_t key = quad_min<P>(best[g2][jl][half]);
+          const int e = ((h0 + 2 * g2 + half) << K) | (jj * J + jl);
+          if (P == 1 || p == 0) cout[e] = (uint16_t)(key >> 16);
+          bits |= (key & 0xFFFFu) << (((g2 * J + jl) * 2 + half) * C::BPB);
+        }
+    if (ri < a.store_rows && (P == 1 || p == 0)) {
+      uint8_t* row = tile_bp + (int64_t)ri * C::ROWB;
+      if (C::UNIT_BITS == 32)
+        reinterpret_cast<uint32_t*>(row)[unit] = bits;
+      else
+        reinterpret_cast<uint16_t*>(row)[unit] = (uint16_t)bits;
+    }
+    __syncthreads();
+  }
+
+  const uint16_t* cfin = s_cost[L & 1];
+  if (a.term_costs) {
+    uint16_t* dst = a.term_costs + ((int64_t)tile * 2 + a.cost_slot) * C::E;
+    for (int e = tid; e < C::E; e += C::NT) dst[e] = cfin[e];
+  }
+  if (a.best_edges) {
+    const uint32_t b = block_argmin<C::NT>(cfin, C::E, s_red);
+    if (tid == 0) a.best_edges[(int64_t)tile * a.best_stride] = (int32_t)b;
+  }
+}
+
+// --------------------------------------------------------- generic kernel
+
+constexpr int GEN_NT = 256;
+constexpr int GEN_ROW_WORDS = 1024;  // largest backpointer row: 4 KiB (K = 1..3)
+
+// Reference-structured forward pass for any K (reference_encoder.py:130-204,
+// quantize_kernels.sycl:83-157): per edge, scan branches k = 0..2^K-1 with a
+// strict fp16 '<'; codebook decoded per candidate. Backpointer rows are
+// assembled in LDS (double-buffered) in the same layout as the fast kernel
+// and copied out one step later.
+__global__ void __launch_bounds__(GEN_NT) acs_forward_generic(FwdArgs a, int K) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][32768];
+  __shared__ uint32_t s_row[2][GEN_ROW_WORDS];
+  __shared__ f16 s_w[256];
+  __shared__ uint32_t s_red[GEN_NT / 64];
+
+  const int tile = blockIdx.x;
+  const int L = a.L;
+  const int E = 65536 >> K, KR = 16 - K, NB = 1 << K;
+  const BpLayout lay = exl3::make_layout(K);
+  const int row_words = lay.row_bytes / 4;
+  const float* in = a.in + (int64_t)tile * L;
+  for (int r = threadIdx.x; r < L; r += GEN_NT) s_w[r] = (f16)in[r];
+  const int pre = a.pre_states ? a.pre_states[(int64_t)tile * a.pre_stride] : -1;
+  for (int e = threadIdx.x; e < E; e += GEN_NT) s_cost[0][e] = (pre < 0 || e == pre) ? 0 : 0x7C00;
+  for (int w = threadIdx.x; w < 2 * GEN_ROW_WORDS; w += GEN_NT) (&s_row[0][0])[w] = 0;
+  __syncthreads();
+  uint8_t* tile_bp = a.bp + (int64_t)tile * a.bp_tile_stride;
+  int prev_ri = -1;
+
+  for (int i = 0; i < L; ++i) {
+    int ri = i + a.roll;
+    if (ri >= L) ri -= L;
+    const uint16_t* cin = s_cost[i & 1];
+    uint16_t* cout = s_cost[(i & 1) ^ 1];
+    uint32_t* row = s_row[i & 1];
+    uint32_t* done = s_row[(i & 1) ^ 1];
+    // Flush the previous step's row (complete since the last barrier) and
+    // clear it for the step after this one.
+    if (prev_ri >= 0) {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(tile_bp + (int64_t)prev_ri * lay.row_bytes);
+      for (int w = threadIdx.x; w < row_words; w += GEN_NT) {
+        if (prev_ri < a.store_rows) dst[w] = done[w];
+        done[w] = 0;
+      }
+    }
+    const f16 w = s_w[ri];
+    for (int e = threadIdx.x; e < E; e += GEN_NT) {
+      f16 best = 0;
+      int best_k = 0;
+      for (int k = 0; k < NB; ++k) {
+        const uint32_t sigma = ((uint32_t)k << KR) | (uint32_t)e;
+        const f16 dh = decode_state(a.cb, sigma) - w;
+        const f16 err = __builtin_fmaf16(dh, dh, f16_bits(cin[sigma >> K]));
+        if (k == 0 || err < best) {
+          best = err;
+          best_k = k;
+        }
+      }
+      cout[e] = bits_f16(best);
+      const uint32_t bit = exl3::bp_slot(lay, (uint32_t)e) * (uint32_t)lay.BPB;
+      if (best_k) atomicOr(&row[bit >> 5], (uint32_t)best_k << (bit & 31u));
+    }
+    prev_ri = ri;
+    __syncthreads();
+  }
+  {
+    const uint32_t* last = s_row[(L - 1) & 1];
+    uint32_t* dst = reinterpret_cast<uint32_t*>(tile_bp + (int64_t)prev_ri * lay.row_bytes);
+    if (prev_ri < a.store_rows)
+      for (int w = threadIdx.x; w < row_words; w += GEN_NT) dst[w] = last[w];
+  }
+
+  const uint16_t* cfin = s_cost[L & 1];
+  if (a.term_costs) {
+    uint16_t* dst = a.term_costs + ((int64_t)tile * 2 + a.cost_slot) * E;
+    for (int e = threadIdx.x; e < E; e += GEN_NT) dst[e] = cfin[e];
+  }
+  if (a.best_edges) {
+    const uint32_t b = block_argmin<GEN_NT>(cfin, E, s_red);
+    if (threadIdx.x == 0) a.best_edges[(int64_t)tile * a.best_stride] = (int32_t)b;
+  }
+}
+
+// Terminal argmin from stored costs (the split API's backward pass reads
+// temp_costs, quantize_kernels.sycl:459-461).
+__global__ void __launch_bounds__(256) argmin_costs_kernel(const uint16_t* __restrict__ costs,
+                                                           int E, int cost_slot,
+                                                           int32_t* __restrict__ out) {
+  __shared__ uint32_t s_red[4];
+  const uint16_t* c = costs + ((int64_t)blockIdx.x * 2 + cost_slot) * E;
+  const uint32_t b = block_argmin<256>(c, E, s_red);
+  if (threadIdx.x == 0) out[blockIdx.x] = (int32_t)b;
+}
+
+// -------------------------------------------------------------- traceback
+
+__device__ __forceinline__ uint32_t read_backpointer(const uint8_t* row, const BpLayout& l,
+                                                     uint32_t edge) {
+  const uint32_t bit = exl3::bp_slot(l, edge) * (uint32_t)l.BPB;
+  const uint32_t word = reinterpret_cast<const uint32_t*>(row)[bit >> 5];
+  return (word >> (bit & 31u)) & ((1u << l.BPB) - 1u);
+}
+
+// Walk back over the ring (reference backward, reference_encoder.py:216-251;
+// quantize_kernels.sycl:320-333,345-358). write = 0: stop after ring row 0
+// and emit the edge reached (the tail-biting end state). write = 1: emit
+// every state and its codebook value.
+__global__ void traceback_kernel(const uint8_t* __restrict__ bp, int64_t bp_tile_stride,
+                                 BpLayout lay, int n, int L, int roll, int write,
+                                 const int32_t* __restrict__ start, int64_t start_stride,
+                                 int32_t* __restrict__ end_out, int64_t end_stride,
+                                 float* __restrict__ out_w, int16_t* __restrict__ out_idx,
+                                 int cb) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const int K = lay.K, KR = 16 - K;
+  const uint8_t* tile_bp = bp + (int64_t)t * bp_tile_stride;
+  // Start edges can come from the caller (split API); keep them in range.
+  uint32_t edge = (uint32_t)start[(int64_t)t * start_stride] & ((65536u >> K) - 1u);
+  for (int i = L - 1; i >= 0; --i) {
+    int ri = i + roll;
+    if (ri >= L) ri -= L;
+    const uint32_t k = read_backpointer(tile_bp + (int64_t)ri * lay.row_bytes, lay, edge);
+    const uint32_t sigma = (k << KR) | edge;
+    if (write) {
+      out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
+      out_w[(int64_t)t * L + ri] = (float)decode_state(cb, sigma);
+    }
+    edge = sigma >> K;
+    if (!write && ri == 0) break;
+  }
+  if (!write) end_out[(int64_t)t * end_stride] = (int32_t)edge;
+}
+
+// ---------------------------------------------------------- prepare/finalize
+
+__global__ void prepare_kernel(const float* __restrict__ raw, float* __restrict__ out, int64_t n,
+                               int L, int permute) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n * L) return;
+  const int64_t t = idx / L;
+  const int i = (int)(idx - t * L);
+  const float v = raw[t * L + (permute ? tc_perm(i) : i)];
+  out[idx] = (float)(f16)v;
+}
+
+// numpy float32 pairwise summation of a block of n in [8, 128] elements
+// (eight accumulators, numpy/_core/src/umath/loops_utils.h.src).
+__device__ float pairwise_block(const float* a, int n) {
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = a[j];
+  int i = 8;
+  for (; i < n - (n % 8); i += 8)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] += a[i + j];
+  float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  for (; i < n; ++i) res += a[i];
+  return res;
+}
+
+// np.sum over n in [16, 256] float32 values: 0 + pairwise(n) where blocks
+// above 128 split at (n/2 rounded down to a multiple of 8).
+__device__ float numpy_sum_f32(const float* a, int n) {
+  if (n <= 128) return 0.0f + pairwise_block(a, n);
+  int n2 = n / 2;
+  n2 -= n2 % 8;
+  return 0.0f + (pairwise_block(a, n2) + pairwise_block(a + n2, n - n2));
+}
+
+__global__ void finalize_kernel(const float* __restrict__ x, const float* __restrict__ raw,
+                                const float* __restrict__ out_w,
+                                const int16_t* __restrict__ out_idx, uint16_t* __restrict__ packed,
+                                float* __restrict__ path_cost, float* __restrict__ distortion,
+                                uint16_t* __restrict__ recon_orig, int64_t n, int K, int L,
+                                int permuted) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const float* xt = x + t * L;
+  const float* wt = out_w + t * L;
+  const int16_t* it = out_idx + t * L;
+
+  // Path cost along the chosen states in ring order (xpu_quantizer.py:933-941).
+  f16 acc = 0;
+  for (int i = 0; i < L; ++i) {
+    const f16 dh = (f16)wt[i] - (f16)xt[i];
+    acc = __builtin_fmaf16(dh, dh, i == 0 ? (f16)0 : acc);
+  }
+  path_cost[t] = (float)acc;
+
+  // Squared error in evaluation order (reference_encoder.py:302-311).
+  float sq[256];
+  for (int pidx = 0; pidx < L; ++pidx) {
+    const int src = permuted ? tc_perm_inv(pidx) : pidx;
+    const f16 rec = (f16)wt[src];
+    if (recon_orig) recon_orig[t * L + pidx] = bits_f16(rec);
+    const float orig = permuted ? raw[t * L + pidx] : xt[pidx];
+    const float d = orig - (float)rec;
+    sq[pidx] = d * d;
+  }
+  distortion[t] = numpy_sum_f32(sq, L);
+
+  // pack_trellis + swap16_storage (trellis_format.py:120-174).
+  if (packed && L == 256) {
+    uint16_t* o = packed + t * 16 * K;
+    for (int span = 0; span < 16; ++span) {
+      uint32_t buf = 0;
+      int held = 32, j = span * K;
+      for (int e = 0; e < 16; ++e) {
+        held -= K;
+        buf |= ((uint32_t)(uint16_t)it[span * 16 + e] & ((1u << K) - 1u)) << held;
+        if (held <= 16) {
+          o[j ^ 1] = (uint16_t)(buf >> 16);  // j ^ 1: half-word swap of each pair
+          buf <<= 16;
+          held += 16;
+          ++j;
+        }
+      }
+    }
+  }
+}
+
+__global__ void pack_kernel(const int16_t* __restrict__ states, uint16_t* __restrict__ packed,
+                            int64_t n, int K) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n * 16) return;
+  const int64_t t = gid >> 4;
+  const int span = (int)(gid & 15);
+  const int16_t* it = states + t * 256 + span * 16;
+  uint16_t* o = packed + t * 16 * K;
+  uint32_t buf = 0;
+  int held = 32, j = span * K;
+  for (int e = 0; e < 16; ++e) {
+    held -= K;
+    buf |= ((uint32_t)(uint16_t)it[e] & ((1u << K) - 1u)) << held;
+    if (held <= 16) {
+      o[j ^ 1] = (uint16_t)(buf >> 16);
+      buf <<= 16;
+      held += 16;
+      ++j;
+    }
+  }
+}
+
+__global__ void probe_hfma_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ c,
+                                  uint16_t* __restrict__ out, int64_t n, int mode) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const f16 x = f16_bits(a[i]), y = f16_bits(c[i]);
+  f16 r;
+  if (mode == 0) {
+    r = __builtin_fmaf16(x, x, y);
+  } else {
+    const f16 sq = x * x;  // rounded product (fp-contract is off)
+    r = sq + y;
+  }
+  out[i] = bits_f16(r);
+}
+
+// =================================================================== host
+
+static hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+static int validate_common(int K, int cb, int L) {
+  if (K < 1 || K > 8) return set_error("K must be in 1..8, got %d", K);
+  if (cb < 0 || cb > 2) return set_error("cb must be 0, 1, or 2, got %d", cb);
+  if (L != 256 && L != 160) return set_error("tile length L must be 256 or 160, got %d", L);
+  if (L == 160 && cb != 2) return set_error("tile length L=160 is only supported with mul1 (cb=2)");
+  return 0;
+}
+
+static bool use_generic(int K, int generic) { return generic || !exl3::has_fast_kernel(K); }
+
+static BpLayout layout_for(int K) { return exl3::make_layout(K); }
+
+template <int K>
+static void launch_fast(const FwdArgs& a, hipStream_t st) {
+  constexpr int G = (K == 1) ? 16 : (K <= 4 ? 4 : 2);
+  constexpr int J = (K == 1) ? 2 : (K == 2 ? 4 : (K == 3 ? 2 : 1));
+  constexpr int P = (K == 6) ? 2 : (K == 7 ? 4 : 1);
+  hipLaunchKernelGGL((acs_forward_fast<K, G, J, P>), dim3(a.n), dim3(1024), 0, st, a);
+}
+
+static int launch_forward(const FwdArgs& a, int K, int generic, hipStream_t st) {
+  if (a.n <= 0) return 0;
+  if (use_generic(K, generic)) {
+    hipLaunchKernelGGL(acs_forward_generic, dim3(a.n), dim3(GEN_NT), 0, st, a, K);
+  } else {
+    switch (K) {
+      case 1: launch_fast<1>(a, st); break;
+      case 2: launch_fast<2>(a, st); break;
+      case 3: launch_fast<3>(a, st); break;
+      case 4: launch_fast<4>(a, st); break;
+      case 5: launch_fast<5>(a, st); break;
+      case 6: launch_fast<6>(a, st); break;
+      case 7: launch_fast<7>(a, st); break;
+      default: return set_error("no fast kernel for K=%d", K);
+    }
+  }
+  return check_launch("acs_forward");
+}
+
+static int launch_traceback(const uint8_t* bp, int64_t stride, const BpLayout& lay, int n, int L,
+                            int roll, int write, const int32_t* start, int64_t start_stride,
+                            int32_t* end_out, int64_t end_stride, float* out_w,
+                            int16_t* out_idx, int cb, hipStream_t st) {
+  if (n <= 0) return 0;
+  const int block = 64;
+  hipLaunchKernelGGL(traceback_kernel, dim3((n + block - 1) / block), dim3(block), 0, st, bp,
+                     stride, lay, n, L, roll, write, start, start_stride, end_out, end_stride,
+                     out_w, out_idx, cb);
+  return check_launch("traceback");
+}
+
+extern "C" {
+
+const char* exl3_last_error(void) { return g_last_error.c_str(); }
+
+const char* exl3_version(void) { return EXL3_VERSION; }
+
+int exl3_decode_codebook(int cb, uint16_t* lut, void* stream) {
+  if (cb < 0 || cb > 2) return set_error("cb must be 0, 1, or 2, got %d", cb);
+  if (!lut) return set_error("lut must not be NULL");
+  hipLaunchKernelGGL(decode_codebook_kernel, dim3(256), dim3(256), 0, as_stream(stream), cb, lut);
+  return check_launch("decode_codebook");
+}
+
+int64_t exl3_scratch_row_bytes(int K) {
+  if (K < 1 || K > 8) return set_error("K must be in 1..8, got %d", K), -1;
+  return layout_for(K).row_bytes;
+}
+
+int64_t exl3_scratch_edges_bytes(int K, int L, int64_t tiles) {
+  if (K < 1 || K > 8 || L <= 0 || tiles < 0) return set_error("bad scratch arguments"), -1;
+  return (int64_t)exl3::tile_scratch_bytes(layout_for(K), L) * tiles;
+}
+
+int64_t exl3_backpointer_slot(int K, int64_t edge) {
+  if (K < 1 || K > 8 || edge < 0 || edge >= (65536 >> K)) return set_error("bad edge"), -1;
+  return exl3::bp_slot(layout_for(K), (uint32_t)edge);
+}
+
+int exl3_forward_pass(const float* in, uint16_t* temp_costs, uint8_t* temp_edges,
+                      const int32_t* pre_states, int64_t n, int K, int cb, int L, int roll,
+                      int cost_slot, int generic, void* stream) {
+  if (validate_common(K, cb, L)) return 1;
+  if (n <= 0 || n > INT32_MAX) return set_error("num_tiles must be positive, got %lld", (long long)n);
+  if (cost_slot != 0 && cost_slot != 1) return set_error("cost_slot must be 0 or 1");
+  if (roll < 0 || roll >= L) return set_error("roll must be in [0, L), got %d", roll);
+  if (!in || !temp_costs || !temp_edges || !pre_states) return set_error("NULL buffer");
+  const BpLayout lay = layout_for(K);
+  FwdArgs a{};
+  a.in = in;
+  a.n = (int)n;
+  a.L = L;
+  a.roll = roll;
+  a.store_rows = L;
+  a.cb = cb;
+  a.pre_states = pre_states;
+  a.pre_stride = 1;
+  a.bp = temp_edges;
+  a.bp_tile_stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
+  a.term_costs = temp_costs;
+  a.cost_slot = cost_slot;
+  a.best_edges = nullptr;
+  return launch_forward(a, K, generic, as_stream(stream));
+}
+
+int exl3_backward_pass(const uint16_t* temp_costs, const uint8_t* temp_edges, float* out_w,
+                       int16_t* out_idx, int32_t* end_states, int64_t n, int K, int cb, int L,
+                       int roll, int cost_slot, int write, void* stream) {
+  if (validate_common(K, cb, L)) return 1;
+  if (n <= 0 || n > INT32_MAX) return set_error("num_tiles must be positive, got %lld", (long long)n);
+  if (cost_slot != 0 && cost_slot != 1) return set_error("cost_slot must be 0 or 1");
+  if (roll < 0 || roll >= L) return set_error("roll must be in [0, L), got %d", roll);
+  if (!temp_costs || !temp_edges || !end_states) return set_error("NULL buffer");
+  if (write && (!out_w || !out_idx)) return set_error("NULL output buffer");
+  const BpLayout lay = layout_for(K);
+  const int64_t stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
+  hipStream_t st = as_stream(stream);
+  if (!write) {
+    const int E = 65536 >> K;
+    hipLaunchKernelGGL(argmin_costs_kernel, dim3((unsigned)n), dim3(256), 0, st, temp_costs, E,
+                       cost_slot, end_states);
+    if (check_launch("argmin_costs")) return 1;
+    return launch_traceback(temp_edges, stride, lay, (int)n, L, roll, 0, end_states, 1,
+                            end_states, 1, nullptr, nullptr, cb, st);
+  }
+  return launch_traceback(temp_edges, stride, lay, (int)n, L, roll, 1, end_states, 1, nullptr, 1,
+                          out_w, out_idx, cb, st);
+}
+
+int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_t* temp_costs,
+                        uint8_t* temp_edges, int64_t batch_cap, int64_t n, int K, int cb, int L,
+                        int generic, int64_t wave_cap, void* stream) {
+  if (validate_common(K, cb, L)) return 1;
+  if (n <= 0) return set_error("num_tiles must be positive, got %lld", (long long)n);
+  if (batch_cap < 1) return set_error("temp_costs batch dimension B must be >= 1");
+  if (!in || !out_w || !out_idx || !temp_costs || !temp_edges) return set_error("NULL buffer");
+  const BpLayout lay = layout_for(K);
+  const int64_t stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
+  // Header row of each tile: int32 {pass-1 terminal edge, end state}.
+  const int64_t hdr = (int64_t)L * lay.row_bytes;
+  const int64_t hstride = stride / 4;
+  int32_t* best_edges = reinterpret_cast<int32_t*>(temp_edges + hdr);
+  int32_t* end_states = best_edges + 1;
+  const int64_t cap = (wave_cap > 0) ? std::min(batch_cap, wave_cap) : batch_cap;
+  const int64_t chunk_max = std::min<int64_t>(cap, INT32_MAX);
+  hipStream_t st = as_stream(stream);
+
+  for (int64_t off = 0; off < n; off += chunk_max) {
+    const int chunk = (int)std::min<int64_t>(chunk_max, n - off);
+    FwdArgs a{};
+    a.in = in + off * L;
+    a.n = chunk;
+    a.L = L;
+    a.cb = cb;
+    a.bp = temp_edges;
+    a.bp_tile_stride = stride;
+    a.term_costs = temp_costs;
+    // Pass 1: rotation L/2, unconstrained; only ring rows 0..L/2-1 are read
+    // back (reference_encoder.py:284-288).
+    a.roll = L / 2;
+    a.store_rows = L / 2;
+    a.pre_states = nullptr;
+    a.cost_slot = 0;
+    a.best_edges = best_edges;
+    a.best_stride = hstride;
+    if (launch_forward(a, K, generic, st)) return 1;
+    if (launch_traceback(temp_edges, stride, lay, chunk, L, L / 2, 0, best_edges, hstride,
+                         end_states, hstride, nullptr, nullptr, cb, st))
+      return 1;
+    // Pass 2: natural order, wrap constrained to the end state (:290-293).
+    a.roll = 0;
+    a.store_rows = L;
+    a.pre_states = end_states;
+    a.pre_stride = hstride;
+    a.cost_slot = 1;
+    a.best_edges = nullptr;
+    if (launch_forward(a, K, generic, st)) return 1;
+    if (launch_traceback(temp_edges, stride, lay, chunk, L, 0, 1, end_states, hstride, nullptr,
+                         1, out_w + off * L, out_idx + off * L, cb, st))
+      return 1;
+  }
+  return 0;
+}
+
+int exl3_prepare_tiles(const float* raw, float* out, int64_t n, int L, int permute,
+                       void* stream) {
+  if (n <= 0 || L <= 0) return set_error("bad tile batch shape");
+  if (permute && L != 256) return set_error("pre_permute=True is only defined for L=256");
+  const int64_t total = n * L;
+  const int block = 256;
+  hipLaunchKernelGGL(prepare_kernel, dim3((unsigned)((total + block - 1) / block)), dim3(block), 0,
+                     as_stream(stream), raw, out, n, L, permute);
+  return check_launch("prepare_tiles");
+}
+
+int exl3_finalize_tiles(const float* x, const float* raw, const float* out_w,
+                        const int16_t* out_idx, uint16_t* packed, float* path_cost,
+                        float* distortion, uint16_t* recon_orig, int64_t n, int K, int L,
+                        int permuted, void* stream) {
+  if (n <= 0 || K < 1 || K > 8 || (L != 256 && L != 160)) return set_error("bad finalize shape");
+  if (permuted && (L != 256 || !raw)) return set_error("permuted finalize needs L=256 raw tiles");
+  if (!x || !out_w || !out_idx || !path_cost || !distortion) return set_error("NULL buffer");
+  const int block = 64;
+  hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)((n + block - 1) / block)), dim3(block), 0,
+                     as_stream(stream), x, raw, out_w, out_idx, packed, path_cost, distortion,
+                     recon_orig, n, K, L, permuted);
+  return check_launch("finalize_tiles");
+}
+
+int exl3_pack_trellis(const int16_t* states, uint16_t* packed, int64_t n, int K, void* stream) {
+  if (n <= 0 || K < 1 || K > 8) return set_error("bad pack arguments");
+  const int64_t total = n * 16;
+  const int block = 256;
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((total + block - 1) / block)), dim3(block), 0,
+                     as_stream(stream), states, packed, n, K);
+  return check_launch("pack_trellis");
+}
+
+int exl3_probe_hfma(const uint16_t* a, const uint16_t* c, uint16_t* out, int64_t n, int mode,
+                    void* stream) {
+  if (n <= 0) return set_error("n must be positive");
+  const int block = 256;
+  hipLaunchKernelGGL(probe_hfma_kernel, dim3((unsigned)((n + block - 1) / block)), dim3(block), 0,
+                     as_stream(stream), a, c, out, n, mode);
+  return check_launch("probe_hfma");
+}
+
+}  // extern "C"

@@ -1,0 +1,570 @@
+"""MI355X tile encoder and bounded scratch arena (PyTorch-ROCm front end).
+
+Counterpart of the reference's exl3_quant/xpu_quantizer.py with the same
+public names — ``build_quantize_extension``, ``get_build_timings``,
+``verify_tile_encoding_quality``, ``ScratchArenaLogEntry``, ``ScratchArena``,
+``BatchEncodingBreakdown``, ``XPUTrellisEncoder`` — so ldlq/layer_quant/
+converter-style callers work unchanged, with ``cuda:i`` devices instead of
+``xpu:i``. ``GPUTrellisEncoder`` is an alias of ``XPUTrellisEncoder``.
+
+Every encoder result (states, reconstruction, packed words, path cost,
+distortion) is computed by the HIP kernels of ``libexl3_hip.so``; the host
+only moves arrays and builds the per-tile ``EncodingResult`` records. There
+is no CPU fallback.
+
+Deviations from the reference, all deliberate:
+
+* scratch layout: ``temp_edges`` is ``uint8 (B, L+1, ROWB)`` K-bit
+  backpointers (include/exl3_encoder.h), sized by the new ScratchEstimator;
+* the arena's default batch capacity is 8192 tiles (the reference used 64 for
+  the Arc iGPU), enough for several waves of 1024-thread workgroups on 256 CUs;
+* traceback placement: ``gpu_resident`` runs the fused encoder;
+  ``gpu_resident_split``, ``d2h_cpu`` and ``usm_host`` run the split
+  forward/traceback passes on the GPU (the host modes existed to work around
+  a slow device traceback on Arc); all four give identical results;
+* ``sg_size`` is validated and ignored (wave64); ``force_global_costs=True``
+  selects the reference-structured generic kernel;
+* NaN inputs are rejected with ``ValueError``: the reference's NaN handling
+  (a NaN at branch 0 sticks) has no counterpart in the integer-key minimum,
+  and its numpy and SYCL encoders already disagree on NaN
+  (docs/algorithm_contract.md:292). Finite and infinite inputs are bit-exact.
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass
+from typing import Callable, List, Optional, Tuple
+
+import numpy as np
+
+from . import build as _build
+from ._native import QuantizeExtension, load_library
+from .memory_policy import MemoryPolicy, MemoryPressureError, capture_snapshot
+from .reference_encoder import EncodingResult
+from .scratch_estimator import ScratchEstimator, backpointer_row_bytes
+from .trellis_format import (CB_3INST, CB_MCG, CB_MUL1, codebook_lut, tensor_core_perm,
+                             tensor_core_perm_inv)
+
+TRACEBACK_MODES = ("gpu_resident", "gpu_resident_split", "d2h_cpu", "usm_host")
+
+_EXT: Optional[QuantizeExtension] = None
+_COLD_BUILD_SECONDS = 0.0
+_WARM_LOAD_SECONDS = 0.0
+
+
+def build_quantize_extension(verbose: bool = False, force_rebuild: bool = False):
+    """Load (or, with ``force_rebuild``, first compile) the native encoder
+    (xpu_quantizer.py:65-98). Raises when the library is missing."""
+    global _EXT, _COLD_BUILD_SECONDS, _WARM_LOAD_SECONDS
+    if _EXT is not None and not force_rebuild:
+        return _EXT
+    t0 = time.perf_counter()
+    if force_rebuild:
+        _build.build_native(force=True, verbose=verbose)
+        _COLD_BUILD_SECONDS = _build.last_build_seconds()
+    lib = load_library()
+    _EXT = QuantizeExtension(lib)
+    if not force_rebuild:
+        _WARM_LOAD_SECONDS = time.perf_counter() - t0
+    return _EXT
+
+
+def get_build_timings() -> dict:
+    return {"cold_build_seconds": _COLD_BUILD_SECONDS, "warm_load_seconds": _WARM_LOAD_SECONDS}
+
+
+def verify_tile_encoding_quality(result: EncodingResult, reference: EncodingResult,
+                                 cost_atol: float = 0.0, distortion_rtol: float = 1e-4) -> dict:
+    """Tie-aware comparison of two encodings (xpu_quantizer.py:108-169): ring
+    continuity, exact codebook reconstruction, end-state consistency, path
+    cost within ``cost_atol`` and distortion within ``distortion_rtol``."""
+    L = len(result.output_indices)
+    K = result.K
+    mask = (65536 >> K) - 1
+    idx = np.asarray(result.output_indices).astype(np.int64)
+    nxt = np.roll(idx, -1)
+    breaks = np.flatnonzero((idx & mask) != (nxt >> K))
+    ring_valid = breaks.size == 0
+    broken_step = int(breaks[0]) if breaks.size else -1
+    lut = codebook_lut(result.cb)
+    rec_exact = bool(np.array_equal(np.asarray(result.reconstructed_perm).view(np.uint16),
+                                    lut[idx].view(np.uint16)))
+    end_state_valid = (int(idx[L - 1]) & mask) == result.end_state
+    indices_identical = bool(np.array_equal(result.output_indices, reference.output_indices))
+    cost_diff = abs(float(result.path_cost) - float(reference.path_cost))
+    cost_ok = cost_diff <= cost_atol
+    ref_dist = max(1e-12, float(reference.distortion))
+    dist_rel_diff = abs(float(result.distortion) - float(reference.distortion)) / ref_dist
+    dist_ok = dist_rel_diff <= distortion_rtol or cost_diff == 0.0
+    return {
+        "passed": ring_valid and rec_exact and end_state_valid and cost_ok and dist_ok,
+        "indices_identical": indices_identical,
+        "ring_valid": ring_valid,
+        "broken_step": broken_step,
+        "rec_exact": rec_exact,
+        "end_state_valid": end_state_valid,
+        "cost_diff": cost_diff,
+        "distortion_rel_diff": dist_rel_diff,
+    }
+
+
+@dataclass
+class ScratchArenaLogEntry:
+    """One arena action with its memory context (xpu_quantizer.py:172-185)."""
+
+    action: str                     # "allocate", "reuse", "evict", "retry-shrink", "release"
+    k: int
+    tile_len: int
+    requested_b: int
+    admitted_b: int
+    scratch_bytes: int
+    distinct_staging_bytes: int
+    outstanding_xpu_bytes: int
+    usable_budget_bytes: int
+    snapshot: dict
+
+
+class ScratchArena:
+    """Bounded single-slot scratch arena for ``temp_costs``/``temp_edges``
+    (xpu_quantizer.py:188-506): at most one buffer pair is resident; a change
+    of (device, K, L) or a larger request synchronises the stream and releases
+    it; a failed admission or allocation halves B down to 1."""
+
+    def __init__(self, policy: Optional[MemoryPolicy] = None, device_index: int = 0,
+                 default_cap_b: int = 8192):
+        self.policy = policy or MemoryPolicy()
+        self.device_index = device_index
+        self.default_cap_b = default_cap_b
+        self._key: Optional[Tuple[int, int, int, int]] = None
+        self._temp_costs = None
+        self._temp_edges = None
+        self.history: List[ScratchArenaLogEntry] = []
+        self.high_water_scratch_bytes = 0
+        self.evictions = 0
+        self.reuses = 0
+        self.allocations = 0
+        self.retries = 0
+
+    @property
+    def current_key(self):
+        return self._key
+
+    @property
+    def resident_bytes(self) -> int:
+        if self._temp_costs is None or self._temp_edges is None:
+            return 0
+        return int(self._temp_costs.numel() * self._temp_costs.element_size()
+                   + self._temp_edges.numel() * self._temp_edges.element_size())
+
+    def _log(self, action, k, t, req, adm, scratch, staging, out_bytes, usable, snap):
+        self.history.append(ScratchArenaLogEntry(
+            action=action, k=k, tile_len=t, requested_b=req, admitted_b=adm,
+            scratch_bytes=scratch, distinct_staging_bytes=staging,
+            outstanding_xpu_bytes=out_bytes, usable_budget_bytes=usable,
+            snapshot=snap.as_dict()))
+
+    def adaptive_batch_capacity(self, k: int, tile_len: int = 256,
+                                requested_b: Optional[int] = None,
+                                distinct_staging_bytes: int = 0) -> int:
+        """Largest admissible B (xpu_quantizer.py:234-269)."""
+        import torch
+
+        target_b = requested_b if requested_b is not None else self.default_cap_b
+        if target_b < 1:
+            raise ValueError(f"requested_b must be >= 1, got {target_b}")
+        snap = capture_snapshot(self.device_index)
+        outstanding = max(0, int(torch.cuda.memory_allocated(self.device_index))
+                          - self.resident_bytes) + distinct_staging_bytes
+        usable = self.policy.usable_bytes(snap, outstanding_bytes=outstanding)
+        per_b = ScratchEstimator.estimate_scratch(k=k, b=1, t=tile_len)
+        max_by_budget = usable // per_b.total_bytes
+        if self.policy.max_single_alloc_bytes is not None:
+            max_by_budget = min(max_by_budget,
+                                self.policy.max_single_alloc_bytes // max(1, per_b.edges_bytes))
+        if max_by_budget < 1:
+            self.policy.check(per_b.total_bytes, snap, outstanding_bytes=outstanding,
+                              context=f"adaptive_batch_capacity K={k} B=1")
+        return int(max(1, min(target_b, max_by_budget)))
+
+    def release(self) -> None:
+        import torch
+
+        if self._temp_costs is None and self._temp_edges is None:
+            return
+        torch.cuda.synchronize(self.device_index)
+        k, t, b = (self._key[1], self._key[2], self._key[3]) if self._key else (0, 0, 0)
+        self._temp_costs = None
+        self._temp_edges = None
+        self._key = None
+        torch.cuda.empty_cache()
+        snap = capture_snapshot(self.device_index)
+        out_bytes = int(torch.cuda.memory_allocated(self.device_index))
+        self._log("release", k, t, b, 0, 0, 0, out_bytes,
+                  self.policy.usable_bytes(snap, out_bytes), snap)
+
+    def acquire(self, k: int, tile_len: int = 256, requested_b: Optional[int] = None,
+                distinct_staging_bytes: int = 0,
+                allocator_hook: Optional[Callable[[int], None]] = None):
+        """Return ``(temp_costs, temp_edges, admitted_b)`` (xpu_quantizer.py:313-506)."""
+        import torch
+
+        target_b = requested_b if requested_b is not None else self.default_cap_b
+        if target_b < 1:
+            raise ValueError(f"requested_b must be >= 1, got {target_b}")
+
+        if (self._key is not None and self._key[0] == self.device_index and self._key[1] == k
+                and self._key[2] == tile_len and self._key[3] >= target_b
+                and self._temp_costs is not None and self._temp_edges is not None):
+            torch.cuda.synchronize(self.device_index)
+            self.reuses += 1
+            snap = capture_snapshot(self.device_index)
+            out_bytes = int(torch.cuda.memory_allocated(self.device_index))
+            self._log("reuse", k, tile_len, target_b, target_b, self.resident_bytes,
+                      distinct_staging_bytes, out_bytes,
+                      self.policy.usable_bytes(snap, out_bytes + distinct_staging_bytes), snap)
+            return self._temp_costs[:target_b], self._temp_edges[:target_b], target_b
+
+        if self._temp_costs is not None or self._temp_edges is not None:
+            self.evictions += 1
+            self.release()
+
+        cand_b = target_b
+        last_err: Optional[Exception] = None
+        rb = backpointer_row_bytes(k)
+        while cand_b >= 1:
+            est = ScratchEstimator.estimate_scratch(k=k, b=cand_b, t=tile_len)
+            snap = capture_snapshot(self.device_index)
+            out_bytes = int(torch.cuda.memory_allocated(self.device_index))
+            effective_outstanding = out_bytes + distinct_staging_bytes
+            costs = edges = None
+            try:
+                self.policy.check(max(est.costs_bytes, est.edges_bytes), snap,
+                                  outstanding_bytes=effective_outstanding,
+                                  context=f"K={k} B={cand_b} single-buffer ceiling")
+                usable = self.policy.usable_bytes(snap, outstanding_bytes=effective_outstanding)
+                if est.total_bytes > usable:
+                    raise MemoryPressureError(
+                        f"memory-pressure abort [K={k} B={cand_b} scratch admit]: "
+                        f"need {est.total_bytes} B > usable {usable} B",
+                        est.total_bytes, usable, snap, f"K={k} B={cand_b} scratch admit")
+                if allocator_hook is not None:
+                    allocator_hook(cand_b)
+                dev = f"cuda:{self.device_index}"
+                costs = torch.empty((cand_b, 2, est.states), dtype=torch.float16, device=dev)
+                edges = torch.empty((cand_b, tile_len + 1, rb), dtype=torch.uint8, device=dev)
+                post = capture_snapshot(self.device_index)
+                self.policy.check_after_commit(post, pre_snapshot=snap,
+                                               expected_bytes=est.total_bytes,
+                                               context=f"K={k} B={cand_b} post-commit")
+                self._key = (self.device_index, k, tile_len, cand_b)
+                self._temp_costs, self._temp_edges = costs, edges
+                self.allocations += 1
+                self.high_water_scratch_bytes = max(self.high_water_scratch_bytes,
+                                                    est.total_bytes)
+                self._log("allocate", k, tile_len, target_b, cand_b, est.total_bytes,
+                          distinct_staging_bytes,
+                          int(torch.cuda.memory_allocated(self.device_index)), usable, post)
+                return costs, edges, cand_b
+            except Exception as exc:  # noqa: BLE001 - any failure shrinks B
+                if costs is not None or edges is not None:
+                    del costs, edges
+                    costs = edges = None
+                    torch.cuda.empty_cache()
+                last_err = exc
+                if cand_b == 1:
+                    break
+                next_b = max(1, cand_b // 2)
+                self.retries += 1
+                self._log("retry-shrink", k, tile_len, cand_b, next_b, est.total_bytes,
+                          distinct_staging_bytes, out_bytes,
+                          self.policy.usable_bytes(snap, effective_outstanding), snap)
+                cand_b = next_b
+
+        if isinstance(last_err, MemoryPressureError):
+            clean = MemoryPressureError(str(last_err), last_err.need_bytes,
+                                        last_err.usable_bytes, last_err.snapshot,
+                                        last_err.context)
+        else:
+            snap = capture_snapshot(self.device_index)
+            out_bytes = int(torch.cuda.memory_allocated(self.device_index))
+            clean = MemoryPressureError(
+                f"scratch allocation failed even at B=1 for K={k}: {last_err}",
+                ScratchEstimator.estimate_scratch(k=k, b=1, t=tile_len).total_bytes,
+                self.policy.usable_bytes(snap, out_bytes + distinct_staging_bytes), snap,
+                context=f"K={k} B=1 minimum batch failure")
+        del last_err
+        raise clean from None
+
+
+@dataclass
+class BatchEncodingBreakdown:
+    """Batch output and timing split (xpu_quantizer.py:509-526)."""
+
+    results: List[EncodingResult]
+    reconstructed_tiles: np.ndarray      # (N, L) float16, original order when pre-permuted
+    reconstructed_perm: np.ndarray       # (N, L) float16, kernel order
+    output_indices: np.ndarray           # (N, L) uint16
+    admitted_b: int
+    num_chunks: int
+    total_seconds: float
+    search_seconds: float
+    traceback_seconds: float
+    transfer_seconds: float
+    postprocess_seconds: float
+    traceback_mode: str
+    sg_size: int
+    force_global_costs: bool
+    packed: Optional[np.ndarray] = None          # (N, 16K) uint16 storage words
+    path_costs: Optional[np.ndarray] = None      # (N,) float32
+    distortions: Optional[np.ndarray] = None     # (N,) float32
+    end_states: Optional[np.ndarray] = None      # (N,) int64
+
+
+class XPUTrellisEncoder:
+    """MI355X encoder with the reference's API (xpu_quantizer.py:529-994)."""
+
+    def __init__(self, K: int = 2, cb: int = CB_MUL1, tile_len: int = 256,
+                 arena: Optional[ScratchArena] = None, device_index: int = 0,
+                 sg_size: int = 32, force_global_costs: bool = False,
+                 wave_cap_override: int = 0):
+        if not 1 <= K <= 8:
+            raise ValueError(f"K must be between 1 and 8, got {K}")
+        if cb not in (CB_3INST, CB_MCG, CB_MUL1):
+            raise ValueError(f"Unknown codebook {cb}")
+        if tile_len not in (256, 160):
+            raise ValueError(f"tile_len must be 256 or 160, got {tile_len}")
+        if tile_len == 160 and cb != CB_MUL1:
+            raise ValueError("tile_len=160 is only supported with CB_MUL1")
+        if sg_size not in (16, 32):
+            raise ValueError(f"sg_size must be 16 or 32, got {sg_size}")
+        self.K = K
+        self.cb = cb
+        self.L = tile_len
+        self.edges = 65536 >> K
+        self.device_index = device_index
+        self.sg_size = sg_size
+        self.force_global_costs = force_global_costs
+        self.wave_cap_override = wave_cap_override
+        self.arena = arena or ScratchArena(device_index=device_index)
+        self._lut = None
+        if self.L == 256:
+            self.perm = tensor_core_perm()
+            self.inv_perm = tensor_core_perm_inv()
+        else:
+            self.perm = None
+            self.inv_perm = None
+
+    @property
+    def lut(self) -> np.ndarray:
+        """fp16 codebook (decoded on the GPU on first use)."""
+        if self._lut is None:
+            self._lut = codebook_lut(self.cb, self.device_index)
+        return self._lut
+
+    @property
+    def mcg_flag(self) -> bool:
+        return self.cb == CB_MCG
+
+    @property
+    def mul1_flag(self) -> bool:
+        return self.cb == CB_MUL1
+
+    @property
+    def device(self) -> str:
+        return f"cuda:{self.device_index}"
+
+    def encode_tile(self, tile: np.ndarray, pre_permute: bool = True,
+                    traceback_mode: str = "gpu_resident") -> EncodingResult:
+        raw = np.asarray(tile, dtype=np.float32).reshape(-1)
+        if raw.size != self.L:
+            raise ValueError(f"Tile must have {self.L} elements, got {raw.size}")
+        return self.encode_batch_detailed(raw.reshape(1, self.L), pre_permute=pre_permute,
+                                          requested_b=1,
+                                          traceback_mode=traceback_mode).results[0]
+
+    def encode_batch(self, tiles: np.ndarray, pre_permute: bool = True,
+                     requested_b: Optional[int] = None,
+                     traceback_mode: str = "gpu_resident") -> List[EncodingResult]:
+        return self.encode_batch_detailed(tiles, pre_permute=pre_permute,
+                                          requested_b=requested_b,
+                                          traceback_mode=traceback_mode).results
+
+    # ------------------------------------------------------------ device API
+
+    def _flatten(self, arr_shape) -> Tuple[int, int]:
+        if len(arr_shape) == 2:
+            return int(arr_shape[0]), int(arr_shape[1])
+        if len(arr_shape) == 3 and tuple(arr_shape[1:]) == (16, 16) and self.L == 256:
+            return int(arr_shape[0]), 256
+        raise ValueError(f"Unsupported tiles shape {tuple(arr_shape)} for L={self.L}")
+
+    def _check_mode(self, n: int, width: int, pre_permute: bool, mode: str) -> None:
+        if n <= 0:
+            raise ValueError(f"num_tiles must be positive, got {n}")
+        if width != self.L:
+            raise ValueError(f"Expected tile length {self.L}, got {width}")
+        if pre_permute and self.L != 256:
+            raise ValueError("pre_permute=True is only defined for L=256")
+        if mode not in TRACEBACK_MODES:
+            raise ValueError(f"Unknown traceback_mode {mode!r}")
+
+    def _run_chunks(self, ext, x_dev, out_w, out_i, temp_costs, temp_edges, admitted_b, mode,
+                    timings):
+        """Encode x_dev (n, L) kernel-order tiles chunk by chunk."""
+        import torch
+
+        n = x_dev.shape[0]
+        num_chunks = 0
+        if mode == "gpu_resident":
+            # One C-ABI call; the library chunks by the scratch capacity.
+            ts = time.perf_counter()
+            ext.quantize_tiles(x_dev, out_w, out_i, temp_costs[:admitted_b],
+                               temp_edges[:admitted_b], self.K, self.mcg_flag, self.mul1_flag,
+                               self.sg_size, self.force_global_costs, self.wave_cap_override)
+            torch.cuda.synchronize(self.device_index)
+            timings["search"] += time.perf_counter() - ts
+            return -(-n // admitted_b)
+        pre = torch.full((admitted_b,), -1, dtype=torch.int32, device=x_dev.device)
+        ends = torch.empty((admitted_b,), dtype=torch.int32, device=x_dev.device)
+        for start in range(0, n, admitted_b):
+            stop = min(start + admitted_b, n)
+            cn = stop - start
+            num_chunks += 1
+            c_in = x_dev[start:stop]
+            c_costs = temp_costs[:cn]
+            c_edges = temp_edges[:cn]
+            c_w = out_w[start:stop]
+            c_i = out_i[start:stop]
+            ts = time.perf_counter()
+            ext.quantize_tiles_forward_pass(c_in, c_costs, c_edges, pre, self.K, self.mcg_flag,
+                                            self.mul1_flag, self.L // 2, 0, self.sg_size,
+                                            self.force_global_costs)
+            torch.cuda.synchronize(self.device_index)
+            tb = time.perf_counter()
+            ext.quantize_tiles_backward_pass(c_costs, c_edges, c_w, c_i, ends, cn, self.K,
+                                             self.mcg_flag, self.mul1_flag, self.L // 2, 0,
+                                             False, self.sg_size)
+            torch.cuda.synchronize(self.device_index)
+            ts2 = time.perf_counter()
+            ext.quantize_tiles_forward_pass(c_in, c_costs, c_edges, ends, self.K, self.mcg_flag,
+                                            self.mul1_flag, 0, 1, self.sg_size,
+                                            self.force_global_costs)
+            torch.cuda.synchronize(self.device_index)
+            tb2 = time.perf_counter()
+            ext.quantize_tiles_backward_pass(c_costs, c_edges, c_w, c_i, ends, cn, self.K,
+                                             self.mcg_flag, self.mul1_flag, 0, 1, True,
+                                             self.sg_size)
+            torch.cuda.synchronize(self.device_index)
+            te = time.perf_counter()
+            timings["search"] += (tb - ts) + (tb2 - ts2)
+            timings["traceback"] += (ts2 - tb) + (te - tb2)
+        return num_chunks
+
+    def encode_tensor(self, tiles, pre_permute: bool = False, requested_b: Optional[int] = None,
+                      traceback_mode: str = "gpu_resident", finalize: bool = True,
+                      allocator_hook: Optional[Callable[[int], None]] = None) -> dict:
+        """Encode an (n, L) float32 device tensor, keeping every output on the
+        device. Returns a dict of device tensors: ``x`` (kernel-order fp16
+        inputs as f32), ``reconstructed_perm`` (f32, kernel order),
+        ``indices`` (int16 states), and with ``finalize``: ``packed``,
+        ``path_cost``, ``distortion``, ``reconstructed`` (fp16 bits as int16,
+        original order)."""
+        import torch
+
+        if not isinstance(tiles, torch.Tensor) or tiles.device.type != "cuda":
+            raise ValueError("encode_tensor expects a GPU tensor")
+        n, width = self._flatten(tiles.shape)
+        self._check_mode(n, width, pre_permute, traceback_mode)
+        raw = tiles.reshape(n, width).to(torch.float32).contiguous()
+        if torch.isnan(raw).any().item():
+            raise ValueError("NaN tile values are not supported (see module docstring)")
+        ext = build_quantize_extension()
+        timings = {"search": 0.0, "traceback": 0.0}
+        x = torch.empty_like(raw)
+        ext.prepare_tiles(raw, x, pre_permute)
+        desired_b = min(n, requested_b if requested_b is not None else self.arena.default_cap_b)
+        temp_costs, temp_edges, admitted_b = self.arena.acquire(
+            k=self.K, tile_len=self.L, requested_b=desired_b, allocator_hook=allocator_hook)
+        out_w = torch.empty((n, self.L), dtype=torch.float32, device=raw.device)
+        out_i = torch.empty((n, self.L), dtype=torch.int16, device=raw.device)
+        num_chunks = self._run_chunks(ext, x, out_w, out_i, temp_costs, temp_edges, admitted_b,
+                                      traceback_mode, timings)
+        res = {"x": x, "reconstructed_perm": out_w, "indices": out_i, "admitted_b": admitted_b,
+               "num_chunks": num_chunks, "timings": timings}
+        if finalize:
+            tp = time.perf_counter()
+            packed = (torch.empty((n, 16 * self.K), dtype=torch.int16, device=raw.device)
+                      if self.L == 256 else None)
+            path_cost = torch.empty(n, dtype=torch.float32, device=raw.device)
+            distortion = torch.empty(n, dtype=torch.float32, device=raw.device)
+            recon = torch.empty((n, self.L), dtype=torch.int16, device=raw.device)
+            ext.finalize_tiles(x, raw, out_w, out_i, packed, path_cost, distortion, recon,
+                               self.K, pre_permute)
+            torch.cuda.synchronize(self.device_index)
+            timings["finalize"] = time.perf_counter() - tp
+            res.update(packed=packed, path_cost=path_cost, distortion=distortion,
+                       reconstructed=recon)
+        return res
+
+    def encode_batch_detailed(self, tiles: np.ndarray, pre_permute: bool = True,
+                              requested_b: Optional[int] = None,
+                              traceback_mode: str = "gpu_resident",
+                              allocator_hook: Optional[Callable[[int], None]] = None,
+                              build_results: bool = True) -> BatchEncodingBreakdown:
+        """Host-array API (xpu_quantizer.py:611-994). ``build_results=False``
+        skips the per-tile ``EncodingResult`` records (arrays only)."""
+        import torch
+
+        arr = np.asarray(tiles, dtype=np.float32)
+        n, width = self._flatten(arr.shape)
+        self._check_mode(n, width, pre_permute, traceback_mode)
+        flat = np.ascontiguousarray(arr.reshape(n, width))
+        if np.isnan(flat).any():
+            raise ValueError("NaN tile values are not supported (see module docstring)")
+
+        t_total0 = time.perf_counter()
+        t0 = time.perf_counter()
+        raw_dev = torch.from_numpy(flat).to(self.device)
+        torch.cuda.synchronize(self.device_index)
+        t_transfer = time.perf_counter() - t0
+
+        enc = self.encode_tensor(raw_dev, pre_permute=pre_permute, requested_b=requested_b,
+                                 traceback_mode=traceback_mode, finalize=True,
+                                 allocator_hook=allocator_hook)
+        tx = time.perf_counter()
+        idx = enc["indices"].cpu().numpy().view(np.uint16)
+        rec_perm = enc["reconstructed_perm"].cpu().numpy().astype(np.float16)
+        rec = enc["reconstructed"].cpu().numpy().view(np.float16)
+        packed = (enc["packed"].cpu().numpy().view(np.uint16) if enc["packed"] is not None
+                  else np.zeros((n, 0), dtype=np.uint16))
+        path_cost = enc["path_cost"].cpu().numpy()
+        distortion = enc["distortion"].cpu().numpy()
+        t_transfer += time.perf_counter() - tx
+        total_seconds = time.perf_counter() - t_total0
+        del raw_dev, enc["x"]
+
+        t_post0 = time.perf_counter()
+        end_states = idx[:, self.L - 1].astype(np.int64) & (self.edges - 1)
+        results: List[EncodingResult] = []
+        if build_results:
+            for i in range(n):
+                d = float(distortion[i])
+                results.append(EncodingResult(
+                    output_indices=idx[i], reconstructed=rec[i], reconstructed_perm=rec_perm[i],
+                    packed=packed[i], end_state=int(end_states[i]), distortion=d,
+                    mse=d / float(self.L),
+                    path_cost=float(path_cost[i]), K=self.K, cb=self.cb))
+        post = time.perf_counter() - t_post0 + enc["timings"].get("finalize", 0.0)
+        return BatchEncodingBreakdown(
+            results=results, reconstructed_tiles=rec, reconstructed_perm=rec_perm,
+            output_indices=idx, admitted_b=enc["admitted_b"], num_chunks=enc["num_chunks"],
+            total_seconds=total_seconds + (time.perf_counter() - t_post0),
+            search_seconds=enc["timings"]["search"],
+            traceback_seconds=enc["timings"]["traceback"], transfer_seconds=t_transfer,
+            postprocess_seconds=post, traceback_mode=traceback_mode, sg_size=self.sg_size,
+            force_global_costs=self.force_global_costs, packed=packed, path_costs=path_cost,
+            distortions=distortion, end_states=end_states)
+
+
+GPUTrellisEncoder = XPUTrellisEncoder

@@ -1,0 +1,145 @@
+"""Scratch sizing for the MI355X encoder (K-bit backpointer layout).
+
+Counterpart of exl3_quant/scratch_estimator.py:23-172 with the same class
+and method names. The formula changes with the layout
+(include/exl3_encoder.h):
+
+    S      = 65536 >> K                      edges per step
+    BPB    = K rounded up to 1, 2, 4 or 8    bits per backpointer
+    costs  = B * 2 * S * 2                   terminal fp16 costs of both passes
+    edges  = B * (T + 1) * S * BPB / 8       K-bit backpointer rows + header row
+
+The reference's int16 layout, ``B * T * S * 2``, is still available by
+passing ``bytes_per_edge`` explicitly (e.g. to compare the two). Per tile at
+T = 256: K=2 1.0 MiB (reference 8 MiB), K=4 514 KiB (2 MiB), K=6 257 KiB
+(512 KiB).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+BYTES_PER_KIB = 1024
+BYTES_PER_MIB = 1024 ** 2
+BYTES_PER_GIB = 1024 ** 3
+
+BYTES_PER_KB = 1000
+BYTES_PER_MB = 1000 ** 2
+BYTES_PER_GB = 1000 ** 3
+
+
+def backpointer_bits(k: int) -> int:
+    """Bits stored per backpointer field (exl3_layout.h bits_per_backpointer)."""
+    return 4 if k == 3 else (8 if k >= 5 else k)
+
+
+def backpointer_row_bytes(k: int) -> int:
+    """Bytes of one backpointer row (exl3_scratch_row_bytes)."""
+    return (65536 >> k) * backpointer_bits(k) // 8
+
+
+@dataclass(frozen=True)
+class ScratchAllocation:
+    """Memory breakdown of one scratch configuration (scratch_estimator.py:23-59)."""
+
+    k: int
+    states: int
+    t: int
+    b: int
+    bytes_per_cost: int
+    bits_per_edge: int
+    costs_bytes: int
+    edges_bytes: int
+    total_bytes: int
+
+    @property
+    def costs_mib(self) -> float:
+        return self.costs_bytes / BYTES_PER_MIB
+
+    @property
+    def costs_mb(self) -> float:
+        return self.costs_bytes / BYTES_PER_MB
+
+    @property
+    def edges_gib(self) -> float:
+        return self.edges_bytes / BYTES_PER_GIB
+
+    @property
+    def edges_gb(self) -> float:
+        return self.edges_bytes / BYTES_PER_GB
+
+    @property
+    def total_gib(self) -> float:
+        return self.total_bytes / BYTES_PER_GIB
+
+    @property
+    def total_gb(self) -> float:
+        return self.total_bytes / BYTES_PER_GB
+
+
+class ScratchEstimator:
+    """Scratch estimator for the trellis encoder (scratch_estimator.py:62-172)."""
+
+    @staticmethod
+    def get_state_count(k: int) -> int:
+        """S = 65536 >> K (scratch_estimator.py:66-74); the encoder accepts K in 1..8."""
+        if k < 1 or k > 16:
+            raise ValueError(f"Trellis parameter K must be between 1 and 16, got {k}")
+        return 65536 >> k
+
+    @classmethod
+    def estimate_scratch(cls, k: int, t: int = 256, b: int = 256, bytes_per_cost: int = 2,
+                         bytes_per_edge: Optional[int] = None) -> ScratchAllocation:
+        """Scratch bytes for ``b`` tiles of length ``t``. ``bytes_per_edge=None``
+        selects the K-bit layout of this encoder; an explicit value reproduces
+        the reference's ``b*t*S*bytes_per_edge`` formula."""
+        if b <= 0:
+            raise ValueError(f"Batch size B must be positive, got {b}")
+        if t <= 0:
+            raise ValueError(f"Sequence length T must be positive, got {t}")
+        states = cls.get_state_count(k)
+        costs_bytes = b * 2 * states * bytes_per_cost
+        if bytes_per_edge is None:
+            if k > 8:
+                raise ValueError(f"the encoder supports K in 1..8, got {k}")
+            bits = backpointer_bits(k)
+            edges_bytes = b * (t + 1) * backpointer_row_bytes(k)
+        else:
+            bits = 8 * bytes_per_edge
+            edges_bytes = b * t * states * bytes_per_edge
+        return ScratchAllocation(k=k, states=states, t=t, b=b, bytes_per_cost=bytes_per_cost,
+                                 bits_per_edge=bits, costs_bytes=costs_bytes,
+                                 edges_bytes=edges_bytes, total_bytes=costs_bytes + edges_bytes)
+
+    @classmethod
+    def calculate_max_batch_size(
+        cls,
+        k: int,
+        available_vram_bytes: int,
+        vram_reserve_bytes: int = 8 * BYTES_PER_GIB,
+        max_single_alloc_bytes: Optional[int] = None,
+        t: int = 256,
+        bytes_per_cost: int = 2,
+        bytes_per_edge: Optional[int] = None,
+    ) -> Tuple[int, ScratchAllocation]:
+        """Largest B that fits ``available - reserve`` and the optional
+        single-allocation ceiling (scratch_estimator.py:114-172). The MI355X
+        defaults: 8 GiB reserve of 288 GB HBM3E, no single-allocation ceiling."""
+        usable = available_vram_bytes - vram_reserve_bytes
+        if usable <= 0:
+            raise ValueError(
+                f"Available VRAM ({available_vram_bytes / BYTES_PER_GIB:.2f} GiB) must exceed "
+                f"reserve ({vram_reserve_bytes / BYTES_PER_GIB:.2f} GiB)")
+        one = cls.estimate_scratch(k=k, t=t, b=1, bytes_per_cost=bytes_per_cost,
+                                   bytes_per_edge=bytes_per_edge)
+        max_b = usable // one.total_bytes
+        if max_single_alloc_bytes is not None:
+            max_b = min(max_b, max_single_alloc_bytes // one.edges_bytes)
+        if max_b < 1:
+            raise ValueError(
+                f"Insufficient memory: minimum batch size B=1 requires "
+                f"{one.total_bytes / BYTES_PER_MIB:.2f} MiB, which exceeds allowable memory budget.")
+        return int(max_b), cls.estimate_scratch(k=k, t=t, b=int(max_b),
+                                                bytes_per_cost=bytes_per_cost,
+                                                bytes_per_edge=bytes_per_edge)

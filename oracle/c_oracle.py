@@ -59,6 +59,17 @@ def lib():
     return _LIB
 
 
+def default_threads() -> int:
+    """OMP_NUM_THREADS when set (the GPU box pins it), else the CPUs this
+    process may run on."""
+    env = os.environ.get("EXL3_ORACLE_THREADS") or os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    if hasattr(os, "sched_getaffinity"):
+        return len(os.sched_getaffinity(0))
+    return os.cpu_count() or 1
+
+
 def codebook_lut(cb: int) -> np.ndarray:
     out = np.empty(65536, dtype=np.uint16)
     lib().exl3o_codebook_lut(int(cb), out)
@@ -129,7 +140,7 @@ def encode_tiles(tiles: np.ndarray, K: int, cb: int = 2, pre_permute: bool = Fal
     end = np.empty(n, dtype=np.int32)
     pc = np.empty(n, dtype=np.uint16)
     best = np.empty(n, dtype=np.int32)
-    threads = threads or int(os.environ.get("EXL3_ORACLE_THREADS", "0")) or (os.cpu_count() or 1)
+    threads = threads or default_threads()
     rc = lib().exl3o_encode_tiles(x16.view(np.uint16), n, K, cb, L, idx, rec, end, pc, best,
                                   threads)
     if rc != 0:

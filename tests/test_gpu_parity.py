@@ -1,0 +1,315 @@
+"""GPU parity: the HIP encoder through the C-ABI against the reference's golden
+vectors and the C oracle (bit-exact), mirroring the reference's device tests
+(tests/test_xpu_quantizer.py of alpha2beta/EXL3_Intel_Arc_quantizer).
+
+Run on an MI355X:  python -u -m pytest tests -m gpu -x -v --timeout 120
+"""
+
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+
+from oracle import c_oracle
+from oracle.trellis_format_ref import codebook_lut as oracle_lut
+from oracle.trellis_format_ref import decode_states
+
+from .conftest import load_golden
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+    return torch
+
+
+@pytest.fixture(scope="module")
+def ext():
+    from exl3_intel_arc_quantizer_amd.gpu_quantizer import build_quantize_extension
+    return build_quantize_extension()
+
+
+def _encoder(**kw):
+    from exl3_intel_arc_quantizer_amd.gpu_quantizer import XPUTrellisEncoder
+    return XPUTrellisEncoder(**kw)
+
+
+def _assert_bd_matches(bd, g, sel, K):
+    np.testing.assert_array_equal(bd.output_indices, g["output_indices"][sel])
+    np.testing.assert_array_equal(bd.end_states, g["end_state"][sel])
+    np.testing.assert_array_equal(bd.path_costs.astype(np.float64), g["path_cost"][sel])
+    np.testing.assert_array_equal(bd.distortions.astype(np.float64), g["distortion"][sel])
+    if bd.packed.shape[1]:
+        np.testing.assert_array_equal(bd.packed, g["packed"][sel][:, :16 * K])
+    np.testing.assert_array_equal(bd.reconstructed_tiles.view(np.uint16),
+                                  g["reconstructed"][sel])
+    np.testing.assert_array_equal(bd.reconstructed_perm.view(np.uint16),
+                                  g["reconstructed_perm"][sel])
+
+
+def test_codebook_bit_exact(ext, torch_mod):
+    """tests/test_xpu_quantizer.py:75-86."""
+    for cb in (0, 1, 2):
+        out = torch_mod.empty(65536, dtype=torch_mod.float16, device="cuda")
+        ext.decode_codebook(cb, out)
+        torch_mod.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16),
+                                      oracle_lut(cb).view(np.uint16))
+
+
+def test_fp16_fma_probe(ext, torch_mod):
+    """The 11 adversarial pairs and 65536 random pairs of xpu_probe.py:153-272:
+    v_fma_f16 rounds once, subnormals kept."""
+    from .test_oracle_known_answers import ADV_COST, ADV_DH
+    rng = np.random.default_rng(2026)
+    dh = np.concatenate([np.array(ADV_DH, dtype=np.uint16).view(np.float16),
+                         rng.normal(0.0, 1.0, size=65536).astype(np.float16)])
+    cost = np.concatenate([np.array(ADV_COST, dtype=np.uint16).view(np.float16),
+                           (rng.random(65536) * 8.0).astype(np.float16)])
+    want = c_oracle.fma_f16(dh, cost).view(np.uint16)
+    a = torch_mod.from_numpy(dh).cuda()
+    c = torch_mod.from_numpy(cost).cuda()
+    out = torch_mod.empty_like(a)
+    ext.probe_hfma(a, c, out, 0)
+    torch_mod.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), want)
+
+
+def test_config1_golden():
+    """64 tiles, K=2, mul1, kernel order: every field bit-exact."""
+    g = load_golden("c1_k2_mul1")
+    enc = _encoder(K=2, cb=2)
+    try:
+        bd = enc.encode_batch_detailed(g["tiles"], pre_permute=False)
+    finally:
+        enc.arena.release()
+    _assert_bd_matches(bd, g, slice(None), 2)
+    # Upstream's K=2 MSE ceiling (tests/test_upstream_encode_oracle.py:56-65).
+    assert np.mean((g["tiles"] - bd.reconstructed_perm.astype(np.float32)) ** 2) < 0.1
+    r = bd.results[5]
+    assert r.end_state == g["end_state"][5] and r.path_cost == g["path_cost"][5]
+
+
+@pytest.mark.parametrize("generic", [False, True])
+def test_k_sweep_golden(generic):
+    """K=1..8 x 3 codebooks x both tile orders (tests/test_xpu_quantizer.py:88-115)."""
+    g = load_golden("k_sweep")
+    for K in range(1, 9):
+        for cb in (0, 1, 2):
+            enc = _encoder(K=K, cb=cb, force_global_costs=generic)
+            try:
+                for pp in (False, True):
+                    sel = (g["K"] == K) & (g["cb"] == cb) & (g["pre_permute"] == pp)
+                    print(f"K={K} cb={cb} pre_permute={pp} generic={generic}", flush=True)
+                    bd = enc.encode_batch_detailed(g["tiles"][sel], pre_permute=pp)
+                    _assert_bd_matches(bd, g, sel, K)
+            finally:
+                enc.arena.release()
+
+
+@pytest.mark.parametrize("name", ["heavy_tail", "edge_cases", "l160"])
+def test_other_golden_sets(name):
+    """Heavy tails at K=2..6, the edge cases of tests/test_xpu_quantizer.py:160-204
+    (zeros, constant, outliers, alternating, overflow, +inf, subnormals) and L=160."""
+    g = load_golden(name)
+    n = g["tiles"].shape[0]
+    Ks = np.atleast_1d(g["K"])
+    pps = np.atleast_1d(g["pre_permute"])
+    L = int(g["L"])
+    for K in np.unique(Ks):
+        for pp in np.unique(pps):
+            sel = (Ks == K if Ks.size == n else np.ones(n, bool)) & \
+                  (pps == pp if pps.size == n else np.ones(n, bool))
+            if not sel.any():
+                continue
+            print(f"{name} K={K} pre_permute={pp}", flush=True)
+            enc = _encoder(K=int(K), cb=int(g["cb"]), tile_len=L)
+            try:
+                bd = enc.encode_batch_detailed(g["tiles"][sel], pre_permute=bool(pp))
+            finally:
+                enc.arena.release()
+            np.testing.assert_array_equal(bd.output_indices, g["output_indices"][sel])
+            np.testing.assert_array_equal(bd.end_states, g["end_state"][sel])
+            np.testing.assert_array_equal(bd.path_costs.astype(np.float64), g["path_cost"][sel])
+            with np.errstate(invalid="ignore"):
+                np.testing.assert_array_equal(bd.distortions.astype(np.float64),
+                                              g["distortion"][sel])
+            if L == 256:
+                np.testing.assert_array_equal(bd.packed, g["packed"][sel][:, :16 * int(K)])
+
+
+def _pred_table(temp_edges_row_block, K, L):
+    """Decode one tile's K-bit backpointer rows into the reference's
+    predecessor-edge table (L, E) uint16."""
+    from exl3_intel_arc_quantizer_amd import _native
+    from exl3_intel_arc_quantizer_amd.scratch_estimator import backpointer_bits
+    lib = _native.load_library()
+    E = 65536 >> K
+    bpb = backpointer_bits(K)
+    slots = np.array([lib.exl3_backpointer_slot(K, e) for e in range(E)], dtype=np.int64)
+    rows = temp_edges_row_block[:L]
+    bits = slots * bpb
+    byte = rows[:, bits // 8].astype(np.int64)
+    k = (byte >> (bits % 8)) & ((1 << bpb) - 1)
+    e = np.arange(E)
+    return ((k << (16 - 2 * K)) | (e >> K)).astype(np.uint16)
+
+
+@pytest.mark.parametrize("generic", [False, True])
+def test_forward_pass_pins(ext, torch_mod, generic):
+    """Split forward pass (quantize_xpu.cpp:169-215) against the reference's
+    forward(): terminal costs bit-exact and the full predecessor table hash."""
+    from exl3_intel_arc_quantizer_amd._native import row_bytes
+    g = load_golden("forward_pass")
+    for i in range(4):
+        K, roll, pre, best, end = (int(v) for v in g[f"case{i}_meta"])
+        print(f"forward case {i}: K={K} roll={roll} pre={pre} generic={generic}", flush=True)
+        x = torch_mod.from_numpy(g[f"case{i}_tile"].view(np.float16).astype(np.float32)).cuda()
+        x = x.reshape(1, 256)
+        E = 65536 >> K
+        costs = torch_mod.zeros((1, 2, E), dtype=torch_mod.float16, device="cuda")
+        edges = torch_mod.zeros((1, 257, row_bytes(K)), dtype=torch_mod.uint8, device="cuda")
+        pre_t = torch_mod.full((1,), pre, dtype=torch_mod.int32, device="cuda")
+        ext.quantize_tiles_forward_pass(x, costs, edges, pre_t, K, False, True, roll, 1, 32,
+                                        generic)
+        ends = torch_mod.zeros((1,), dtype=torch_mod.int32, device="cuda")
+        w = torch_mod.zeros((1, 256), dtype=torch_mod.float32, device="cuda")
+        idx = torch_mod.zeros((1, 256), dtype=torch_mod.int16, device="cuda")
+        ext.quantize_tiles_backward_pass(costs, edges, w, idx, ends, 1, K, False, True, roll, 1,
+                                         False)
+        torch_mod.cuda.synchronize()
+        np.testing.assert_array_equal(costs[0, 1].cpu().numpy().view(np.uint16),
+                                      g[f"case{i}_costs"])
+        table = _pred_table(edges[0].cpu().numpy(), K, 256)
+        np.testing.assert_array_equal(table[:4, :64], g[f"case{i}_edges_head"])
+        assert hashlib.sha256(table.tobytes()).hexdigest() == str(g[f"case{i}_edges_sha256"])
+        assert int(ends.item()) == end
+
+
+def test_traceback_modes_and_variants_agree():
+    """tests/test_xpu_quantizer.py:299-330."""
+    rng = np.random.default_rng(909)
+    tiles = rng.normal(0.0, 1.1, size=(4, 256)).astype(np.float32)
+    ref = c_oracle.encode_tiles(tiles, K=2, cb=2, pre_permute=True)
+    for mode in ("gpu_resident", "gpu_resident_split", "d2h_cpu", "usm_host"):
+        enc = _encoder(K=2, cb=2)
+        try:
+            bd = enc.encode_batch_detailed(tiles, requested_b=4, traceback_mode=mode)
+        finally:
+            enc.arena.release()
+        np.testing.assert_array_equal(bd.output_indices, ref.output_indices, err_msg=mode)
+    for sg in (16, 32):
+        for fg in (False, True):
+            enc = _encoder(K=2, cb=2, sg_size=sg, force_global_costs=fg)
+            try:
+                bd = enc.encode_batch_detailed(tiles, requested_b=4)
+            finally:
+                enc.arena.release()
+            np.testing.assert_array_equal(bd.output_indices, ref.output_indices)
+
+
+def test_batches_partial_chunks_and_waves():
+    """tests/test_xpu_quantizer.py:206-235: 19 tiles, B=6, wave cap 4."""
+    rng = np.random.default_rng(555)
+    tiles = rng.normal(0.0, 1.0, size=(19, 256)).astype(np.float32)
+    ref = c_oracle.encode_tiles(tiles, K=3, cb=2, pre_permute=True)
+    for mode in ("gpu_resident", "gpu_resident_split"):
+        enc = _encoder(K=3, cb=2, wave_cap_override=4)
+        try:
+            bd = enc.encode_batch_detailed(tiles, requested_b=6, traceback_mode=mode)
+        finally:
+            enc.arena.release()
+        assert bd.admitted_b == 6 and bd.num_chunks == 4 and len(bd.results) == 19
+        np.testing.assert_array_equal(bd.output_indices, ref.output_indices)
+        for t in range(19):
+            np.testing.assert_array_equal(decode_states(bd.results[t].packed, 3),
+                                          bd.output_indices[t])
+
+
+def test_queue_ordering_and_async(ext, torch_mod):
+    """tests/test_xpu_quantizer.py:271-297: torch ops before/after the encoder
+    on the same stream, no host sync in between."""
+    rng = np.random.default_rng(808)
+    raw = rng.normal(0.0, 0.5, size=(4, 256)).astype(np.float16).astype(np.float32)
+    from exl3_intel_arc_quantizer_amd._native import row_bytes
+    in_t = torch_mod.from_numpy(raw).cuda()
+    in_t.mul_(2.0)
+    out_w = torch_mod.empty_like(in_t)
+    out_i = torch_mod.empty((4, 256), dtype=torch_mod.int16, device="cuda")
+    costs = torch_mod.empty((4, 2, 8192), dtype=torch_mod.float16, device="cuda")
+    edges = torch_mod.empty((4, 257, row_bytes(3)), dtype=torch_mod.uint8, device="cuda")
+    ext.quantize_tiles(in_t, out_w, out_i, costs, edges, 3, False, True)
+    out_w.add_(1.0)
+    torch_mod.cuda.synchronize()
+    ref = c_oracle.encode_tiles(raw * 2.0, K=3, cb=2, pre_permute=False)
+    np.testing.assert_array_equal(out_i.cpu().numpy().view(np.uint16), ref.output_indices)
+    np.testing.assert_allclose(out_w.cpu().numpy(),
+                               ref.reconstructed_perm.astype(np.float32) + 1.0, atol=1e-5)
+
+
+def test_extension_rejects_malformed_tensors(ext, torch_mod):
+    """tests/test_xpu_quantizer.py:260-269."""
+    from exl3_intel_arc_quantizer_amd._native import row_bytes
+    in_t = torch_mod.zeros((1, 256), dtype=torch_mod.float32, device="cuda")
+    out_w = torch_mod.zeros((1, 256), dtype=torch_mod.float32, device="cuda")
+    out_i = torch_mod.zeros((1, 256), dtype=torch_mod.int16, device="cuda")
+    costs = torch_mod.zeros((1, 2, 16384), dtype=torch_mod.float16, device="cuda")
+    edges = torch_mod.zeros((1, 257, row_bytes(2)), dtype=torch_mod.uint8, device="cuda")
+    with pytest.raises(RuntimeError):
+        ext.quantize_tiles(in_t, out_w, out_i, costs, edges, 2, True, True)
+    with pytest.raises(RuntimeError):
+        ext.quantize_tiles(in_t.cpu(), out_w, out_i, costs, edges, 2, False, True)
+    with pytest.raises(RuntimeError):
+        ext.quantize_tiles(in_t, out_w, out_i, costs, edges[:, :256], 2, False, True)
+    with pytest.raises(RuntimeError):
+        ext.quantize_tiles(in_t, out_w, out_i.float(), costs, edges, 2, False, True)
+
+
+def test_config2_subsample_vs_c_oracle(torch_mod):
+    """Config 2: a 1024x1024 N(0,1) fp16 matrix, tiles formed as ldlq.py:276-281
+    (16-row blocks, tensor-core permuted), K=4; every 32nd tile bit-exact."""
+    rng = np.random.default_rng(1)
+    W = rng.standard_normal((1024, 1024), dtype=np.float32).astype(np.float16).astype(np.float32)
+    tiles = W.reshape(64, 16, 64, 16).transpose(0, 2, 1, 3).reshape(4096, 256)
+    enc = _encoder(K=4, cb=2)
+    try:
+        bd = enc.encode_batch_detailed(tiles, pre_permute=True, build_results=False)
+    finally:
+        enc.arena.release()
+    sub = np.arange(0, 4096, 32)
+    ref = c_oracle.encode_tiles(tiles[sub], K=4, cb=2, pre_permute=True)
+    np.testing.assert_array_equal(bd.output_indices[sub], ref.output_indices)
+    np.testing.assert_array_equal(bd.packed[sub], ref.packed)
+    np.testing.assert_array_equal(bd.distortions[sub], ref.distortion)
+
+
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 6])
+def test_large_batch_invariants(K):
+    """Config-3-style heavy-tailed tiles at scale: size-independent properties
+    (ring continuity, tail biting, recon == lut[idx], packing round trip,
+    path cost, MSE ceilings) over 8192 tiles, plus 16 tiles bit-exact."""
+    rng = np.random.default_rng(2 + K)
+    x = rng.standard_normal((8192, 256), dtype=np.float32)
+    x = np.where(rng.random(x.shape) < 0.01, 4.0 * x, x).astype(np.float16).astype(np.float32)
+    enc = _encoder(K=K, cb=2)
+    try:
+        bd = enc.encode_batch_detailed(x, pre_permute=False, build_results=False)
+    finally:
+        enc.arena.release()
+    idx = bd.output_indices.astype(np.int64)
+    mask = (65536 >> K) - 1
+    np.testing.assert_array_equal(idx & mask, np.roll(idx, -1, axis=1) >> K)
+    np.testing.assert_array_equal(bd.end_states, idx[:, 255] & mask)
+    lut = oracle_lut(2)
+    np.testing.assert_array_equal(bd.reconstructed_perm.view(np.uint16), lut[idx].view(np.uint16))
+    for t in range(0, 8192, 1021):
+        np.testing.assert_array_equal(decode_states(bd.packed[t], K), idx[t])
+    assert np.all(np.isfinite(bd.path_costs)) and np.all(bd.path_costs > 0)
+    sub = np.arange(0, 8192, 512)
+    ref = c_oracle.encode_tiles(x[sub], K=K, cb=2, pre_permute=False)
+    np.testing.assert_array_equal(bd.output_indices[sub], ref.output_indices)
+    np.testing.assert_array_equal(bd.path_costs[sub], ref.path_cost)

@@ -1,0 +1,132 @@
+"""Host-side logic that needs no GPU: scratch sizing, memory policy, the
+tensor-core permutation table, and argument validation of the encoder and
+extension facade (reference tests/test_scratch.py, tests/test_memory_policy.py,
+tests/test_xpu_quantizer.py:237-269)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from exl3_intel_arc_quantizer_amd import trellis_format
+from exl3_intel_arc_quantizer_amd.gpu_quantizer import XPUTrellisEncoder
+from exl3_intel_arc_quantizer_amd._native import QuantizeExtension
+from exl3_intel_arc_quantizer_amd.memory_policy import (
+    BYTES_PER_GIB, MemoryPolicy, MemoryPressureError, capture_snapshot, default_reserve_bytes,
+    read_system_memory, reflect_outstanding_counters)
+from exl3_intel_arc_quantizer_amd.scratch_estimator import (
+    BYTES_PER_MIB, ScratchEstimator, backpointer_bits, backpointer_row_bytes)
+from oracle import trellis_format_ref
+
+
+def test_reference_formula_fixtures_still_reproducible():
+    """tests/test_scratch.py:32-57 of the reference, via bytes_per_edge=2."""
+    for k, states, edges_gib, costs_mib in ((1, 32768, 4.0, 32.0), (2, 16384, 2.0, 16.0),
+                                            (3, 8192, 1.0, 8.0), (4, 4096, 0.5, 4.0)):
+        a = ScratchEstimator.estimate_scratch(k=k, t=256, b=256, bytes_per_edge=2)
+        assert a.states == states
+        assert a.edges_gib == pytest.approx(edges_gib)
+        assert a.costs_mib == pytest.approx(costs_mib)
+
+
+@pytest.mark.parametrize("k,per_tile", [(1, 257 * 4096), (2, 257 * 4096), (3, 257 * 4096),
+                                        (4, 257 * 2048), (5, 257 * 2048), (6, 257 * 1024),
+                                        (7, 257 * 512), (8, 257 * 256)])
+def test_kbit_layout_formula(k, per_tile):
+    a = ScratchEstimator.estimate_scratch(k=k, t=256, b=10)
+    assert a.edges_bytes == 10 * per_tile
+    assert a.costs_bytes == 10 * 2 * (65536 >> k) * 2
+    assert a.total_bytes == a.costs_bytes + a.edges_bytes
+    assert backpointer_row_bytes(k) * 8 == (65536 >> k) * backpointer_bits(k)
+    assert backpointer_bits(k) >= k
+
+
+def test_estimator_validation_and_max_batch():
+    with pytest.raises(ValueError):
+        ScratchEstimator.estimate_scratch(k=0)
+    with pytest.raises(ValueError):
+        ScratchEstimator.estimate_scratch(k=3, b=0)
+    with pytest.raises(ValueError):
+        ScratchEstimator.estimate_scratch(k=3, t=-1)
+    # 288 GB HBM, 8 GiB reserve, K=2: ~1.06 MiB per tile.
+    max_b, alloc = ScratchEstimator.calculate_max_batch_size(k=2, available_vram_bytes=288 * 10 ** 9)
+    assert alloc.total_bytes <= 288 * 10 ** 9 - 8 * BYTES_PER_GIB
+    assert max_b == (288 * 10 ** 9 - 8 * BYTES_PER_GIB) // (257 * 4096 + 2 * 16384 * 2)
+    max_b, _ = ScratchEstimator.calculate_max_batch_size(
+        k=3, available_vram_bytes=64 * BYTES_PER_GIB, max_single_alloc_bytes=16 * BYTES_PER_MIB)
+    assert max_b == 16 * BYTES_PER_MIB // (257 * 4096)
+    with pytest.raises(ValueError):
+        ScratchEstimator.calculate_max_batch_size(k=2, available_vram_bytes=BYTES_PER_GIB)
+
+
+def test_meminfo_parsing_and_policy(tmp_path):
+    p = tmp_path / "meminfo"
+    p.write_text("MemTotal:       1000000 kB\nMemFree:         500000 kB\n"
+                 "MemAvailable:    800000 kB\nCached: 100 kB\nBogus: 5 kB\n")
+    sysmem = read_system_memory(str(p))
+    assert sysmem["MemAvailable"] == 800000 * 1024 and sysmem["SwapTotal"] == 0
+    snap = capture_snapshot(0, meminfo_path=str(p))
+    pol = MemoryPolicy(reserve_bytes=100 * 1024 * 1024, reflect_outstanding=False)
+    if not snap.gpu_available:
+        assert snap.binding_available_bytes == 800000 * 1024
+        usable = pol.usable_bytes(snap, outstanding_bytes=50 * 1024 * 1024)
+        assert usable == 800000 * 1024 - 150 * 1024 * 1024
+        with pytest.raises(MemoryPressureError) as ei:
+            pol.check(10 ** 12, snap, context="unit")
+        assert "unit" in str(ei.value) and ei.value.as_dict()["need_bytes"] == 10 ** 12
+    ceiling = MemoryPolicy(reserve_bytes=0, max_single_alloc_bytes=10)
+    with pytest.raises(MemoryPressureError):
+        ceiling.check(11, snap)
+    with pytest.raises(ValueError):
+        pol.usable_bytes(snap, outstanding_bytes=-1)
+
+
+def test_policy_env_overrides(monkeypatch):
+    monkeypatch.setenv("EXL3_MEMORY_RESERVE_GIB", "1.5")
+    assert default_reserve_bytes() == int(1.5 * BYTES_PER_GIB)
+    monkeypatch.delenv("EXL3_MEMORY_RESERVE_GIB")
+    monkeypatch.setenv("EXL3_MEMORY_RESERVE_BYTES", "12345")
+    assert default_reserve_bytes() == 12345
+    monkeypatch.delenv("EXL3_MEMORY_RESERVE_BYTES")
+    assert default_reserve_bytes() == 8 * BYTES_PER_GIB
+    assert reflect_outstanding_counters() is True
+    monkeypatch.setenv("EXL3_MEMORY_REFLECT_OUTSTANDING", "0")
+    assert reflect_outstanding_counters() is False
+
+
+def test_package_perm_matches_oracle():
+    np.testing.assert_array_equal(trellis_format.tensor_core_perm(),
+                                  trellis_format_ref.tensor_core_perm())
+    np.testing.assert_array_equal(trellis_format.tensor_core_perm_inv(),
+                                  trellis_format_ref.tensor_core_perm_inv())
+
+
+def test_encoder_constructor_validation():
+    """tests/test_xpu_quantizer.py:239-250 of the reference."""
+    for kwargs in ({"K": 0}, {"K": 9}, {"K": 2, "cb": 99}, {"K": 2, "tile_len": 128},
+                   {"K": 2, "cb": 1, "tile_len": 160}, {"K": 2, "sg_size": 8}):
+        with pytest.raises(ValueError):
+            XPUTrellisEncoder(**kwargs)
+    enc = XPUTrellisEncoder(K=2)
+    with pytest.raises(ValueError):
+        enc.encode_tile(np.zeros(100, dtype=np.float32))
+    with pytest.raises(ValueError):
+        enc.encode_batch(np.zeros((0, 256), dtype=np.float32))
+    with pytest.raises(ValueError):
+        enc.encode_batch(np.zeros((2, 256), dtype=np.float32), traceback_mode="bad")
+    with pytest.raises(ValueError):
+        enc.encode_batch(np.full((1, 256), np.nan, dtype=np.float32))
+
+
+def test_extension_validation_without_gpu():
+    """quantize_xpu.cpp:73-101 checks raise RuntimeError."""
+    import torch
+
+    ext = QuantizeExtension()
+    t = torch.zeros((1, 256), dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="ambiguous"):
+        ext.quantize_tiles(t, t, t, t, t, 2, True, True)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ext.quantize_tiles(t, t, t, t, t, 2, False, True)
+    with pytest.raises(RuntimeError, match="cb must be"):
+        ext.decode_codebook(7, torch.zeros(65536, dtype=torch.float16))

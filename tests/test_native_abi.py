@@ -1,0 +1,94 @@
+"""The C-ABI library loads on the CPU, exports every symbol the public header
+declares, and its host-only entry points behave (no GPU work is launched)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from exl3_intel_arc_quantizer_amd import _native, scratch_estimator
+from exl3_intel_arc_quantizer_amd.build import LIB_PATH
+
+from .conftest import REPO_ROOT
+
+HEADER = REPO_ROOT / "include" / "exl3_encoder.h"
+
+
+def _declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(exl3_\w+)\s*\(", text, re.M)))
+
+
+def test_library_built_in_tree():
+    assert LIB_PATH.exists(), "run __graft_entry__.build() first"
+
+
+def test_header_symbols_are_exported():
+    lib = ctypes.CDLL(str(LIB_PATH))
+    declared = _declared_symbols()
+    assert len(declared) >= 13
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in exl3_encoder.h but not exported"
+    assert declared == _native.exported_symbols()
+
+
+def test_version_and_empty_error():
+    lib = _native.load_library()
+    assert lib.exl3_version().decode().startswith("exl3-mi355x")
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+def test_row_bytes_match_estimator(K):
+    lib = _native.load_library()
+    assert lib.exl3_scratch_row_bytes(K) == scratch_estimator.backpointer_row_bytes(K)
+    for L in (256, 160):
+        assert (lib.exl3_scratch_edges_bytes(K, L, 3)
+                == scratch_estimator.ScratchEstimator.estimate_scratch(k=K, t=L, b=3).edges_bytes)
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+def test_backpointer_slots_are_a_permutation(K):
+    """Every edge owns exactly one backpointer field of a row."""
+    lib = _native.load_library()
+    E = 65536 >> K
+    step = max(1, E // 4096)
+    edges = np.arange(0, E, step)
+    slots = np.array([lib.exl3_backpointer_slot(K, int(e)) for e in edges])
+    assert slots.min() >= 0 and slots.max() < E
+    if step == 1:
+        assert np.array_equal(np.sort(slots), np.arange(E))
+    else:
+        assert np.unique(slots).size == edges.size
+    assert lib.exl3_backpointer_slot(K, E) == -1
+
+
+@pytest.mark.parametrize("K,cb,L,msg", [
+    (0, 2, 256, "K must be in 1..8"),
+    (9, 2, 256, "K must be in 1..8"),
+    (2, 3, 256, "cb must be 0, 1, or 2"),
+    (2, 2, 128, "tile length L must be 256 or 160"),
+    (2, 1, 160, "L=160 is only supported with mul1"),
+])
+def test_quantize_rejects_bad_arguments_before_any_gpu_work(K, cb, L, msg):
+    lib = _native.load_library()
+    rc = lib.exl3_quantize_tiles(None, None, None, None, None, 1, 1, K, cb, L, 0, 0, None)
+    assert rc != 0
+    assert msg in lib.exl3_last_error().decode()
+
+
+def test_forward_and_backward_reject_bad_arguments():
+    lib = _native.load_library()
+    assert lib.exl3_forward_pass(None, None, None, None, 1, 2, 2, 256, 300, 0, 0, None) != 0
+    assert "roll" in lib.exl3_last_error().decode()
+    assert lib.exl3_forward_pass(None, None, None, None, 1, 2, 2, 256, 0, 2, 0, None) != 0
+    assert "cost_slot" in lib.exl3_last_error().decode()
+    assert lib.exl3_backward_pass(None, None, None, None, None, 0, 2, 2, 256, 0, 0, 0,
+                                  None) != 0
+    assert "num_tiles" in lib.exl3_last_error().decode()
+    assert lib.exl3_decode_codebook(5, None, None) != 0
+    assert lib.exl3_pack_trellis(None, None, 0, 2, None) != 0
+    assert lib.exl3_prepare_tiles(None, None, 1, 160, 1, None) != 0
+    assert "pre_permute" in lib.exl3_last_error().decode()
