@@ -127,7 +127,7 @@ def cpu_baseline(tiles, K):
     encoder) on a bounded sample of the same workload, all host cores."""
     from oracle import c_oracle
     cores = c_oracle.default_threads()
-    n = max(cores, 2 * cores)
+    n = 16 * cores                                   # ~10 s of CPU work
     sample = tiles[:n]
     c_oracle.encode_tiles(sample[:1], K=K, cb=2, pre_permute=True, threads=1)  # load + warm
     t0 = time.perf_counter()
@@ -145,6 +145,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--sweep", action="store_true", help="also run K=2..6 on configs[2]")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--k-list", default="4,2",
+                    help="bitrates to time on configs[1]; the first is the headline value")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 1 GiB device copy (known-size kernel for PMC byte "
+                         "counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the encoder "
@@ -157,8 +162,19 @@ def main() -> int:
     ext = build_quantize_extension()
     tiles = config2_tiles()
 
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("# calibration copy: 3 x 1 GiB read + 1 GiB written", file=sys.stderr, flush=True)
+        del src, dst
+        torch.cuda.empty_cache()
+
+    k_list = [int(k) for k in args.k_list.split(",")]
     results = {}
-    for K in (4, 2):
+    for K in k_list:
         b = DeviceBatch(tiles, K, torch, ext)
         sec = time_steps(b, args.steps, args.warmup, torch)
         results[K] = {"tiles_per_s": b.n / sec, "ms_per_step": sec * 1e3,
@@ -185,8 +201,9 @@ def main() -> int:
             del b
             torch.cuda.empty_cache()
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(tiles, 4)
-    main_k = results[4]
+    head = k_list[0]
+    cpu = None if args.no_cpu_baseline else cpu_baseline(tiles, head)
+    main_k = results[head]
     line = {
         "metric": METRIC,
         "value": round(main_k["tiles_per_s"], 1),
@@ -201,14 +218,15 @@ def main() -> int:
         "dtype": "fp16",
         "data": "synthetic",
         "config": {"workload": "configs[1]: 1024x1024 N(0,1) fp16 matrix (seed 1), 4096 tiles "
-                               "in LDLQ order, K=4, MUL1, L=256",
-                   "tiles": 4096, "K": 4, "codebook": "mul1"},
+                               f"in LDLQ order, K={head}, MUL1, L=256",
+                   "tiles": 4096, "K": head, "codebook": "mul1"},
         "roofline": main_k["roofline"],
         "cpu_baseline": cpu,
-        "k2": {"value": round(results[2]["tiles_per_s"], 1), "unit": "tiles/s",
-               "ms_per_step": round(results[2]["ms_per_step"], 3),
-               "roofline": results[2]["roofline"]},
     }
+    for K in k_list[1:]:
+        line[f"k{K}"] = {"value": round(results[K]["tiles_per_s"], 1), "unit": "tiles/s",
+                         "ms_per_step": round(results[K]["ms_per_step"], 3),
+                         "roofline": results[K]["roofline"]}
     if sweep is not None:
         line["sweep_configs2"] = sweep
     print(json.dumps(line), flush=True)

@@ -5,18 +5,25 @@
 // and its SYCL kernel FusedQuantizeKernel (quantize_kernels.sycl:245-360),
 // re-designed for CDNA4:
 //
-//   acs_forward_fast   one 1024-thread workgroup per tile; fp16 path costs
-//                      ping-pong in LDS; each thread owns 64 (edge, branch)
-//                      candidates whose codebook values live in 32 VGPRs for
-//                      the whole launch; packed-fp16 subtract/FMA; the
-//                      first-minimum over branches is an unsigned min over
+//   acs_forward_rows   K = 3..7. One 1024-thread workgroup per tile, fp16 path
+//                      costs ping-pong in LDS, each thread owns 64 (edge,
+//                      branch) candidates whose codebook values stay in 32
+//                      VGPRs. A step is three packed-fp16 ops per candidate
+//                      pair (subtract, FMA, unsigned-16 min): the minimum cost
+//                      per edge only. Each step's cost row goes to HBM with
+//                      coalesced 16-byte stores; the traceback recomputes the
+//                      argmin of the one edge on the path.
+//   acs_forward_keys   K = 1, 2 (cost rows would cost 32-64 KiB per step):
+//                      the first minimum over branches is an unsigned min over
 //                      32-bit keys (cost bits << 16 | branch); winning branches
-//                      leave as K-bit backpointers in coalesced 16/32-bit
-//                      stores, only for the ring rows the traceback reads.
+//                      leave as K-bit backpointers.
 //   acs_forward_generic reference-structured kernel (one edge per thread
 //                      iteration, codebook decoded per candidate, strict fp16
-//                      '<' scan): K = 8 and the force_global_costs variant.
-//   traceback_kernel   one lane per tile walks the K-bit backpointers.
+//                      '<' scan): K = 8 and the force_global_costs variant;
+//                      writes the same scratch layout as the fast kernels.
+//   traceback_kernel   walks the ring backwards (one lane per tile over
+//                      backpointers, or 2^K lanes per tile recomputing the
+//                      candidates from cost rows).
 //   finalize_kernel    packing, path cost, distortion, un-permutation.
 //
 // Numerics (bit-exact vs the reference on finite / infinite inputs):
@@ -27,10 +34,11 @@
 //   fma(dh, dh, +inf) == +inf, which is the reference's masked step 0
 //   (reference_encoder.py:152-179).
 //   Costs are non-negative fp16 or +inf, whose bit patterns order like their
-//   values, so min over (cost_bits << 16 | k) picks the lowest k among equal
-//   minima — the reference's "k = 0 initialises, later k replaces only if
-//   strictly smaller" rule (reference_encoder.py:169-176,193-199). NaN inputs
-//   are rejected by the host wrapper (see the package's encoder module).
+//   values, so an unsigned min gives the minimum cost, and a min over
+//   (cost_bits << 16 | k) picks the lowest k among equal minima — the
+//   reference's "k = 0 initialises, later k replaces only if strictly
+//   smaller" rule (reference_encoder.py:169-176,193-199). NaN inputs are
+//   rejected by the host wrapper (see the package's encoder module).
 #include <hip/hip_runtime.h>
 
 #include <stdarg.h>
@@ -149,22 +157,81 @@ __device__ uint32_t block_argmin(const uint16_t* cost, int E, uint32_t* s_red) {
   return s_red[0] & 0xFFFFu;
 }
 
-// Arguments shared by both forward kernels. Tile t of the launch reads
-// in + t*L and owns scratch slot t.
+// Arguments shared by the forward kernels. Tile t of the launch reads
+// in + t*L and owns scratch block t.
 struct FwdArgs {
   const float* in;
-  int n, L, roll, store_rows, cb;
+  int n, L, roll, cb;
+  int store_rows;             // backpointer mode: ring rows ri < store_rows are stored
+  int store_from;             // cost-row mode: step rows i in [store_from, L-2] are stored
   const int32_t* pre_states;  // may be NULL: unconstrained
   int64_t pre_stride;         // in int32 elements
-  uint8_t* bp;                // backpointer scratch, tile stride bp_tile_stride
-  int64_t bp_tile_stride;
-  uint16_t* term_costs;       // [slot][2][E] or NULL
+  uint8_t* scratch;           // per-tile blocks of (L+1) rows
+  int64_t tile_stride;        // bytes per block
+  int64_t hdr_offset;         // byte offset of the header row inside a block
+  uint16_t* term_costs;       // [tile][2][E] or NULL
   int cost_slot;
   int32_t* best_edges;        // terminal argmin per tile or NULL
   int64_t best_stride;
 };
 
-// ------------------------------------------------------------ fast kernel
+// Load the tile's fp16 inputs into LDS, record pre_state (and, for cost rows,
+// the inputs) in the tile header, and set the initial cost vector.
+template <int NT>
+__device__ __forceinline__ void forward_prologue(const FwdArgs& a, int E, bool stash_inputs,
+                                                 f16* s_w, uint16_t* cost0, int& pre_out) {
+  const int tile = blockIdx.x;
+  const float* in = a.in + (int64_t)tile * a.L;
+  uint8_t* hdr = a.scratch + (int64_t)tile * a.tile_stride + a.hdr_offset;
+  for (int r = threadIdx.x; r < a.L; r += NT) {
+    const f16 w = (f16)in[r];
+    s_w[r] = w;
+    if (stash_inputs) reinterpret_cast<uint16_t*>(hdr + exl3::HDR_W_BYTES)[r] = bits_f16(w);
+  }
+  const int pre = a.pre_states ? a.pre_states[(int64_t)tile * a.pre_stride] : -1;
+  if (threadIdx.x == 0) reinterpret_cast<int32_t*>(hdr)[exl3::HDR_PRE_STATE] = pre;
+  for (int e = threadIdx.x; e < E; e += NT) cost0[e] = (pre < 0 || e == pre) ? 0 : 0x7C00;
+  pre_out = pre;
+}
+
+// Terminal costs to temp_costs and the pass-1 terminal argmin.
+template <int NT>
+__device__ __forceinline__ void forward_epilogue(const FwdArgs& a, int E, const uint16_t* cfin,
+                                                 uint32_t* s_red) {
+  const int tile = blockIdx.x;
+  if (a.term_costs) {
+    uint16_t* dst = a.term_costs + ((int64_t)tile * 2 + a.cost_slot) * E;
+    for (int e = threadIdx.x; e < E; e += NT) dst[e] = cfin[e];
+  }
+  if (a.best_edges) {
+    const uint32_t b = block_argmin<NT>(cfin, E, s_red);
+    if (threadIdx.x == 0) a.best_edges[(int64_t)tile * a.best_stride] = (int32_t)b;
+  }
+}
+
+// Copy the cost row of step `step` (held in LDS) to the tile's scratch.
+template <int NT>
+__device__ __forceinline__ void store_cost_row(const FwdArgs& a, int E, const uint16_t* src,
+                                               int step) {
+  const int chunks = E / 8;  // 16-byte chunks
+  uint4* dst = reinterpret_cast<uint4*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
+                                        (int64_t)step * E * 2);
+  const uint4* s = reinterpret_cast<const uint4*>(src);
+  for (int c = threadIdx.x; c < chunks; c += NT) dst[c] = s[c];
+}
+
+// ------------------------------------------------------------ fast kernels
+
+// Thread decomposition per K; exl3_layout.h keeps the same table for the
+// backpointer slots. G groups x J edges x Q branches per lane, P lanes share
+// one edge set and split its 2^K branches; 1024 threads, 64 candidates per
+// thread and step.
+template <int K>
+struct FastShape {
+  static constexpr int G = (K == 1) ? 16 : (K <= 4 ? 4 : 2);
+  static constexpr int J = (K == 1) ? 2 : (K == 2 ? 4 : (K == 3 ? 2 : 1));
+  static constexpr int P = (K == 6) ? 2 : (K == 7 ? 4 : 1);
+};
 
 template <int K, int G, int J, int P>
 struct FastCfg {
@@ -181,7 +248,6 @@ struct FastCfg {
   static constexpr int ROWB = E * BPB / 8;
   static_assert(NT == 1024, "fast configurations use 1024 threads");
   static_assert(G % 2 == 0, "groups are processed in packed pairs");
-  static_assert(UNIT_BITS == 16 || UNIT_BITS == 32, "unit store width");
   static_assert(P == 1 || P == 2 || P == 4, "branch split within a quad");
 };
 
@@ -192,14 +258,54 @@ __device__ __forceinline__ uint32_t quad_min(uint32_t v) {
   return v;
 }
 
-template <int K, int G, int J, int P>
-__global__ void __launch_bounds__(1024) acs_forward_fast(FwdArgs a) {
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+template <int P>
+__device__ __forceinline__ u16x2 quad_min_u16x2(u16x2 v) {
+  if (P >= 2) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(
+        0, (int)__builtin_bit_cast(uint32_t, v), 0xB1, 0xF, 0xF, false);
+    v = __builtin_elementwise_min(v, __builtin_bit_cast(u16x2, o));
+  }
+  if (P >= 4) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(
+        0, (int)__builtin_bit_cast(uint32_t, v), 0x4E, 0xF, 0xF, false);
+    v = __builtin_elementwise_min(v, __builtin_bit_cast(u16x2, o));
+  }
+  return v;
+}
+
+// Codebook values of this thread's candidates: pair (g2, jl, q) holds the
+// states of groups h0+2*g2 (low half) and h0+2*g2+1 (high half), edge
+// j = jj*J + jl, branch k = p*Q + q.
+template <int K, int G, int J, int Q, int KR, int CB>
+__device__ __forceinline__ void load_codebook(f16x2 (&cbv)[G / 2][J][Q], int p, int jj, int h0) {
+#pragma unroll
+  for (int g2 = 0; g2 < G / 2; ++g2)
+#pragma unroll
+    for (int jl = 0; jl < J; ++jl)
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const uint32_t k = (uint32_t)(p * Q + q);
+        const uint32_t j = (uint32_t)(jj * J + jl);
+        const uint32_t s_lo = (k << KR) | ((uint32_t)(h0 + 2 * g2) << K) | j;
+        f16x2 v;
+        v.x = decode_state(CB, s_lo);
+        v.y = decode_state(CB, s_lo + (1u << K));
+        cbv[g2][jl][q] = v;
+      }
+}
+
+// Cost-row forward pass (K = 3..7): minimum cost per edge, rows to HBM.
+// CB is the codebook selector (compile time keeps the prologue's registers
+// low enough for two workgroups per CU).
+template <int K, int G, int J, int P, int CB>
+__global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
   using C = FastCfg<K, G, J, P>;
   __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][C::E];
   __shared__ f16 s_w[256];
   __shared__ uint32_t s_red[16];
 
-  const int tile = blockIdx.x;
   const int L = a.L;
   const int tid = threadIdx.x;
   const int p = tid % P;
@@ -208,32 +314,82 @@ __global__ void __launch_bounds__(1024) acs_forward_fast(FwdArgs a) {
   const int gq = unit / C::NJ;
   const int h0 = gq * G;
 
-  // Codebook values of this thread's candidates: pair (g2, jl, q) holds the
-  // states of groups h0+2*g2 (low half) and h0+2*g2+1 (high half), edge
-  // j = jj*J + jl, branch k = p*Q + q.
   f16x2 cbv[G / 2][J][C::Q];
-#pragma unroll
-  for (int g2 = 0; g2 < G / 2; ++g2)
-#pragma unroll
-    for (int jl = 0; jl < J; ++jl)
-#pragma unroll
-      for (int q = 0; q < C::Q; ++q) {
-        const uint32_t k = (uint32_t)(p * C::Q + q);
-        const uint32_t j = (uint32_t)(jj * J + jl);
-        const uint32_t s_lo = (k << C::KR) | ((uint32_t)(h0 + 2 * g2) << K) | j;
-        f16x2 v;
-        v.x = decode_state(a.cb, s_lo);
-        v.y = decode_state(a.cb, s_lo + (1u << K));
-        cbv[g2][jl][q] = v;
-      }
-
-  const float* in = a.in + (int64_t)tile * L;
-  for (int r = tid; r < L; r += C::NT) s_w[r] = (f16)in[r];
-  const int pre = a.pre_states ? a.pre_states[(int64_t)tile * a.pre_stride] : -1;
-  for (int e = tid; e < C::E; e += C::NT) s_cost[0][e] = (pre < 0 || e == pre) ? 0 : 0x7C00;
+  load_codebook<K, G, J, C::Q, C::KR, CB>(cbv, p, jj, h0);
+  int pre;
+  forward_prologue<C::NT>(a, C::E, true, s_w, s_cost[0], pre);
   __syncthreads();
 
-  uint8_t* tile_bp = a.bp + (int64_t)tile * a.bp_tile_stride;
+  for (int i = 0; i < L; ++i) {
+    int ri = i + a.roll;
+    if (ri >= L) ri -= L;
+    const uint16_t* cin = s_cost[i & 1];
+    uint16_t* cout = s_cost[(i & 1) ^ 1];
+    if (i >= 1 && i - 1 >= a.store_from) store_cost_row<C::NT>(a, C::E, cin, i - 1);
+    const f16 w = s_w[ri];
+    f16x2 w2;
+    w2.x = w;
+    w2.y = w;
+
+    u16x2 m[G / 2][J];
+#pragma unroll
+    for (int q = 0; q < C::Q; ++q) {
+      const uint32_t k = (uint32_t)(p * C::Q + q);
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(cin + k * C::S + h0);
+      uint32_t cpair[G / 2];
+#pragma unroll
+      for (int g2 = 0; g2 < G / 2; ++g2) cpair[g2] = src[g2];
+#pragma unroll
+      for (int g2 = 0; g2 < G / 2; ++g2)
+#pragma unroll
+        for (int jl = 0; jl < J; ++jl) {
+          const f16x2 dh = cbv[g2][jl][q] - w2;
+          const f16x2 err =
+              __builtin_elementwise_fma(dh, dh, __builtin_bit_cast(f16x2, cpair[g2]));
+          const u16x2 eu = __builtin_bit_cast(u16x2, err);
+          m[g2][jl] = (q == 0) ? eu : __builtin_elementwise_min(m[g2][jl], eu);
+        }
+    }
+#pragma unroll
+    for (int g2 = 0; g2 < G / 2; ++g2)
+#pragma unroll
+      for (int jl = 0; jl < J; ++jl) {
+        const u16x2 v = quad_min_u16x2<P>(m[g2][jl]);
+        const int e = ((h0 + 2 * g2) << K) | (jj * J + jl);
+        if (P == 1 || p == 0) {
+          cout[e] = v.x;
+          cout[e + (1 << K)] = v.y;
+        }
+      }
+    __syncthreads();
+  }
+  forward_epilogue<C::NT>(a, C::E, s_cost[L & 1], s_red);
+}
+
+// Key forward pass (K = 1, 2): first minimum over branches with K-bit
+// backpointers in slot order.
+template <int K, int G, int J, int P, int CB>
+__global__ void __launch_bounds__(1024) acs_forward_keys(FwdArgs a) {
+  using C = FastCfg<K, G, J, P>;
+  static_assert(C::UNIT_BITS == 16 || C::UNIT_BITS == 32, "unit store width");
+  __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][C::E];
+  __shared__ f16 s_w[256];
+  __shared__ uint32_t s_red[16];
+
+  const int L = a.L;
+  const int tid = threadIdx.x;
+  const int p = tid % P;
+  const int unit = tid / P;
+  const int jj = unit % C::NJ;
+  const int gq = unit / C::NJ;
+  const int h0 = gq * G;
+
+  f16x2 cbv[G / 2][J][C::Q];
+  load_codebook<K, G, J, C::Q, C::KR, CB>(cbv, p, jj, h0);
+  int pre;
+  forward_prologue<C::NT>(a, C::E, false, s_w, s_cost[0], pre);
+  __syncthreads();
+  uint8_t* tile_bp = a.scratch + (int64_t)blockIdx.x * a.tile_stride;
 
   for (int i = 0; i < L; ++i) {
     int ri = i + a.roll;
@@ -292,46 +448,35 @@ __global__ void __launch_bounds__(1024) acs_forward_fast(FwdArgs a) {
     }
     __syncthreads();
   }
-
-  const uint16_t* cfin = s_cost[L & 1];
-  if (a.term_costs) {
-    uint16_t* dst = a.term_costs + ((int64_t)tile * 2 + a.cost_slot) * C::E;
-    for (int e = tid; e < C::E; e += C::NT) dst[e] = cfin[e];
-  }
-  if (a.best_edges) {
-    const uint32_t b = block_argmin<C::NT>(cfin, C::E, s_red);
-    if (tid == 0) a.best_edges[(int64_t)tile * a.best_stride] = (int32_t)b;
-  }
+  forward_epilogue<C::NT>(a, C::E, s_cost[L & 1], s_red);
 }
 
 // --------------------------------------------------------- generic kernel
 
 constexpr int GEN_NT = 256;
-constexpr int GEN_ROW_WORDS = 1024;  // largest backpointer row: 4 KiB (K = 1..3)
+constexpr int GEN_ROW_WORDS = 1024;  // largest backpointer row: 4 KiB (K = 1, 2)
 
 // Reference-structured forward pass for any K (reference_encoder.py:130-204,
 // quantize_kernels.sycl:83-157): per edge, scan branches k = 0..2^K-1 with a
-// strict fp16 '<'; codebook decoded per candidate. Backpointer rows are
-// assembled in LDS (double-buffered) in the same layout as the fast kernel
-// and copied out one step later.
+// strict fp16 '<'; codebook decoded per candidate. It writes the scratch
+// layout of K: backpointer rows assembled in LDS (double-buffered, copied out
+// one step later), or cost rows.
 __global__ void __launch_bounds__(GEN_NT) acs_forward_generic(FwdArgs a, int K) {
   __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][32768];
   __shared__ uint32_t s_row[2][GEN_ROW_WORDS];
   __shared__ f16 s_w[256];
   __shared__ uint32_t s_red[GEN_NT / 64];
 
-  const int tile = blockIdx.x;
   const int L = a.L;
   const int E = 65536 >> K, KR = 16 - K, NB = 1 << K;
   const BpLayout lay = exl3::make_layout(K);
+  const bool rows = lay.mode == exl3::MODE_COST_ROWS;
   const int row_words = lay.row_bytes / 4;
-  const float* in = a.in + (int64_t)tile * L;
-  for (int r = threadIdx.x; r < L; r += GEN_NT) s_w[r] = (f16)in[r];
-  const int pre = a.pre_states ? a.pre_states[(int64_t)tile * a.pre_stride] : -1;
-  for (int e = threadIdx.x; e < E; e += GEN_NT) s_cost[0][e] = (pre < 0 || e == pre) ? 0 : 0x7C00;
+  int pre;
+  forward_prologue<GEN_NT>(a, E, rows, s_w, s_cost[0], pre);
   for (int w = threadIdx.x; w < 2 * GEN_ROW_WORDS; w += GEN_NT) (&s_row[0][0])[w] = 0;
   __syncthreads();
-  uint8_t* tile_bp = a.bp + (int64_t)tile * a.bp_tile_stride;
+  uint8_t* tile_bp = a.scratch + (int64_t)blockIdx.x * a.tile_stride;
   int prev_ri = -1;
 
   for (int i = 0; i < L; ++i) {
@@ -341,9 +486,11 @@ __global__ void __launch_bounds__(GEN_NT) acs_forward_generic(FwdArgs a, int K) 
     uint16_t* cout = s_cost[(i & 1) ^ 1];
     uint32_t* row = s_row[i & 1];
     uint32_t* done = s_row[(i & 1) ^ 1];
-    // Flush the previous step's row (complete since the last barrier) and
-    // clear it for the step after this one.
-    if (prev_ri >= 0) {
+    if (rows) {
+      if (i >= 1 && i - 1 >= a.store_from) store_cost_row<GEN_NT>(a, E, cin, i - 1);
+    } else if (prev_ri >= 0) {
+      // Flush the previous step's backpointer row (complete since the last
+      // barrier) and clear it for the step after this one.
       uint32_t* dst = reinterpret_cast<uint32_t*>(tile_bp + (int64_t)prev_ri * lay.row_bytes);
       for (int w = threadIdx.x; w < row_words; w += GEN_NT) {
         if (prev_ri < a.store_rows) dst[w] = done[w];
@@ -364,28 +511,20 @@ __global__ void __launch_bounds__(GEN_NT) acs_forward_generic(FwdArgs a, int K) 
         }
       }
       cout[e] = bits_f16(best);
-      const uint32_t bit = exl3::bp_slot(lay, (uint32_t)e) * (uint32_t)lay.BPB;
-      if (best_k) atomicOr(&row[bit >> 5], (uint32_t)best_k << (bit & 31u));
+      if (!rows && best_k) {
+        const uint32_t bit = exl3::bp_slot(lay, (uint32_t)e) * (uint32_t)lay.BPB;
+        atomicOr(&row[bit >> 5], (uint32_t)best_k << (bit & 31u));
+      }
     }
     prev_ri = ri;
     __syncthreads();
   }
-  {
+  if (!rows && prev_ri < a.store_rows) {
     const uint32_t* last = s_row[(L - 1) & 1];
     uint32_t* dst = reinterpret_cast<uint32_t*>(tile_bp + (int64_t)prev_ri * lay.row_bytes);
-    if (prev_ri < a.store_rows)
-      for (int w = threadIdx.x; w < row_words; w += GEN_NT) dst[w] = last[w];
+    for (int w = threadIdx.x; w < row_words; w += GEN_NT) dst[w] = last[w];
   }
-
-  const uint16_t* cfin = s_cost[L & 1];
-  if (a.term_costs) {
-    uint16_t* dst = a.term_costs + ((int64_t)tile * 2 + a.cost_slot) * E;
-    for (int e = threadIdx.x; e < E; e += GEN_NT) dst[e] = cfin[e];
-  }
-  if (a.best_edges) {
-    const uint32_t b = block_argmin<GEN_NT>(cfin, E, s_red);
-    if (threadIdx.x == 0) a.best_edges[(int64_t)tile * a.best_stride] = (int32_t)b;
-  }
+  forward_epilogue<GEN_NT>(a, E, s_cost[L & 1], s_red);
 }
 
 // Terminal argmin from stored costs (the split API's backward pass reads
@@ -408,35 +547,86 @@ __device__ __forceinline__ uint32_t read_backpointer(const uint8_t* row, const B
   return (word >> (bit & 31u)) & ((1u << l.BPB) - 1u);
 }
 
+struct TbArgs {
+  const uint8_t* scratch;
+  int64_t tile_stride, hdr_offset;
+  BpLayout lay;
+  int n, L, roll, write, cb;
+  const int32_t* start;  // start edge per tile
+  int64_t start_stride;
+  int32_t* end_out;      // edge reached at ring row 0 (write = 0)
+  int64_t end_stride;
+  float* out_w;          // write = 1
+  int16_t* out_idx;
+};
+
 // Walk back over the ring (reference backward, reference_encoder.py:216-251;
 // quantize_kernels.sycl:320-333,345-358). write = 0: stop after ring row 0
 // and emit the edge reached (the tail-biting end state). write = 1: emit
 // every state and its codebook value.
-__global__ void traceback_kernel(const uint8_t* __restrict__ bp, int64_t bp_tile_stride,
-                                 BpLayout lay, int n, int L, int roll, int write,
-                                 const int32_t* __restrict__ start, int64_t start_stride,
-                                 int32_t* __restrict__ end_out, int64_t end_stride,
-                                 float* __restrict__ out_w, int16_t* __restrict__ out_idx,
-                                 int cb) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n) return;
-  const int K = lay.K, KR = 16 - K;
-  const uint8_t* tile_bp = bp + (int64_t)t * bp_tile_stride;
-  // Start edges can come from the caller (split API); keep them in range.
-  uint32_t edge = (uint32_t)start[(int64_t)t * start_stride] & ((65536u >> K) - 1u);
-  for (int i = L - 1; i >= 0; --i) {
-    int ri = i + roll;
-    if (ri >= L) ri -= L;
-    const uint32_t k = read_backpointer(tile_bp + (int64_t)ri * lay.row_bytes, lay, edge);
-    const uint32_t sigma = (k << KR) | edge;
-    if (write) {
-      out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
-      out_w[(int64_t)t * L + ri] = (float)decode_state(cb, sigma);
+//
+// Backpointer mode: one lane per tile reads k from the row.
+// Cost-row mode: GL = min(2^K, 64) lanes per tile recompute the candidates
+// of the current edge at step i from cost row i-1 (or the initial costs at
+// i = 0) and take the key minimum (lowest branch among equal costs).
+template <int GL>
+__global__ void __launch_bounds__(256) traceback_kernel(TbArgs a) {
+  const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = gid / GL;
+  const int lane = gid % GL;
+  if (t >= a.n) return;  // whole lane groups leave together
+  const BpLayout& lay = a.lay;
+  const int K = lay.K, KR = 16 - K, L = a.L;
+  const uint8_t* blk = a.scratch + (int64_t)t * a.tile_stride;
+  const uint8_t* hdr = blk + a.hdr_offset;
+  uint32_t edge = (uint32_t)a.start[(int64_t)t * a.start_stride] & ((65536u >> K) - 1u);
+
+  if (lay.mode == exl3::MODE_BACKPOINTERS) {
+    for (int i = L - 1; i >= 0; --i) {
+      int ri = i + a.roll;
+      if (ri >= L) ri -= L;
+      const uint32_t k = read_backpointer(blk + (int64_t)ri * lay.row_bytes, lay, edge);
+      const uint32_t sigma = (k << KR) | edge;
+      if (a.write) {
+        a.out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
+        a.out_w[(int64_t)t * L + ri] = (float)decode_state(a.cb, sigma);
+      }
+      edge = sigma >> K;
+      if (!a.write && ri == 0) break;
     }
-    edge = sigma >> K;
-    if (!write && ri == 0) break;
+  } else {
+    const int NB = 1 << K;
+    const int pre = reinterpret_cast<const int32_t*>(hdr)[exl3::HDR_PRE_STATE];
+    const uint16_t* wbits = reinterpret_cast<const uint16_t*>(hdr + exl3::HDR_W_BYTES);
+    const int E = 65536 >> K;
+    for (int i = L - 1; i >= 0; --i) {
+      int ri = i + a.roll;
+      if (ri >= L) ri -= L;
+      const f16 w = f16_bits(wbits[ri]);
+      const uint16_t* prow = reinterpret_cast<const uint16_t*>(blk) + (int64_t)(i - 1) * E;
+      uint32_t key = 0xFFFFFFFFu;
+      for (int k = lane; k < NB; k += GL) {
+        const uint32_t sigma = ((uint32_t)k << KR) | edge;
+        const uint32_t pred = sigma >> K;
+        const uint16_t cbits =
+            (i == 0) ? ((pre < 0 || (int)pred == pre) ? 0 : 0x7C00) : prow[pred];
+        const f16 dh = decode_state(a.cb, sigma) - w;
+        const f16 err = __builtin_fmaf16(dh, dh, f16_bits(cbits));
+        key = umin(key, ((uint32_t)bits_f16(err) << 16) | (uint32_t)k);
+      }
+#pragma unroll
+      for (int m = GL / 2; m >= 1; m >>= 1)
+        key = umin(key, (uint32_t)__shfl_xor((int)key, m, GL));
+      const uint32_t sigma = ((key & 0xFFFFu) << KR) | edge;
+      if (a.write && lane == 0) {
+        a.out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
+        a.out_w[(int64_t)t * L + ri] = (float)decode_state(a.cb, sigma);
+      }
+      edge = sigma >> K;
+      if (!a.write && ri == 0) break;
+    }
   }
-  if (!write) end_out[(int64_t)t * end_stride] = (int32_t)edge;
+  if (!a.write && lane == 0) a.end_out[(int64_t)t * a.end_stride] = (int32_t)edge;
 }
 
 // ---------------------------------------------------------- prepare/finalize
@@ -580,12 +770,25 @@ static bool use_generic(int K, int generic) { return generic || !exl3::has_fast_
 
 static BpLayout layout_for(int K) { return exl3::make_layout(K); }
 
+template <int K, int CB>
+static void launch_fast_cb(const FwdArgs& a, hipStream_t st) {
+  using Sh = FastShape<K>;
+  if constexpr (K >= 3) {
+    hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB>), dim3(a.n), dim3(1024), 0,
+                       st, a);
+  } else {
+    hipLaunchKernelGGL((acs_forward_keys<K, Sh::G, Sh::J, Sh::P, CB>), dim3(a.n), dim3(1024), 0,
+                       st, a);
+  }
+}
+
 template <int K>
 static void launch_fast(const FwdArgs& a, hipStream_t st) {
-  constexpr int G = (K == 1) ? 16 : (K <= 4 ? 4 : 2);
-  constexpr int J = (K == 1) ? 2 : (K == 2 ? 4 : (K == 3 ? 2 : 1));
-  constexpr int P = (K == 6) ? 2 : (K == 7 ? 4 : 1);
-  hipLaunchKernelGGL((acs_forward_fast<K, G, J, P>), dim3(a.n), dim3(1024), 0, st, a);
+  switch (a.cb) {
+    case 0: launch_fast_cb<K, 0>(a, st); break;
+    case 1: launch_fast_cb<K, 1>(a, st); break;
+    default: launch_fast_cb<K, 2>(a, st); break;
+  }
 }
 
 static int launch_forward(const FwdArgs& a, int K, int generic, hipStream_t st) {
@@ -607,16 +810,57 @@ static int launch_forward(const FwdArgs& a, int K, int generic, hipStream_t st) 
   return check_launch("acs_forward");
 }
 
-static int launch_traceback(const uint8_t* bp, int64_t stride, const BpLayout& lay, int n, int L,
-                            int roll, int write, const int32_t* start, int64_t start_stride,
-                            int32_t* end_out, int64_t end_stride, float* out_w,
-                            int16_t* out_idx, int cb, hipStream_t st) {
-  if (n <= 0) return 0;
-  const int block = 64;
-  hipLaunchKernelGGL(traceback_kernel, dim3((n + block - 1) / block), dim3(block), 0, st, bp,
-                     stride, lay, n, L, roll, write, start, start_stride, end_out, end_stride,
-                     out_w, out_idx, cb);
+static FwdArgs forward_args(const float* in, int n, int K, int cb, int L, uint8_t* scratch,
+                            uint16_t* term_costs) {
+  const BpLayout lay = layout_for(K);
+  FwdArgs a{};
+  a.in = in;
+  a.n = n;
+  a.L = L;
+  a.cb = cb;
+  a.scratch = scratch;
+  a.tile_stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
+  a.hdr_offset = (int64_t)L * lay.row_bytes;
+  a.term_costs = term_costs;
+  a.store_rows = L;
+  a.store_from = 0;
+  return a;
+}
+
+static int launch_traceback(const TbArgs& a, hipStream_t st) {
+  if (a.n <= 0) return 0;
+  const int block = 256;
+  if (a.lay.mode == exl3::MODE_BACKPOINTERS) {
+    hipLaunchKernelGGL(traceback_kernel<1>, dim3((a.n + block - 1) / block), dim3(block), 0, st,
+                       a);
+  } else {
+    const int gl = (1 << a.lay.K) < 64 ? (1 << a.lay.K) : 64;
+    const int64_t threads = (int64_t)a.n * gl;
+    const dim3 grid((unsigned)((threads + block - 1) / block));
+    switch (gl) {
+      case 8: hipLaunchKernelGGL(traceback_kernel<8>, grid, dim3(block), 0, st, a); break;
+      case 16: hipLaunchKernelGGL(traceback_kernel<16>, grid, dim3(block), 0, st, a); break;
+      case 32: hipLaunchKernelGGL(traceback_kernel<32>, grid, dim3(block), 0, st, a); break;
+      default: hipLaunchKernelGGL(traceback_kernel<64>, grid, dim3(block), 0, st, a); break;
+    }
+  }
   return check_launch("traceback");
+}
+
+static TbArgs traceback_args(const uint8_t* scratch, int n, int K, int cb, int L, int roll,
+                             int write) {
+  const BpLayout lay = layout_for(K);
+  TbArgs t{};
+  t.scratch = scratch;
+  t.tile_stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
+  t.hdr_offset = (int64_t)L * lay.row_bytes;
+  t.lay = lay;
+  t.n = n;
+  t.L = L;
+  t.roll = roll;
+  t.write = write;
+  t.cb = cb;
+  return t;
 }
 
 extern "C" {
@@ -655,21 +899,11 @@ int exl3_forward_pass(const float* in, uint16_t* temp_costs, uint8_t* temp_edges
   if (cost_slot != 0 && cost_slot != 1) return set_error("cost_slot must be 0 or 1");
   if (roll < 0 || roll >= L) return set_error("roll must be in [0, L), got %d", roll);
   if (!in || !temp_costs || !temp_edges || !pre_states) return set_error("NULL buffer");
-  const BpLayout lay = layout_for(K);
-  FwdArgs a{};
-  a.in = in;
-  a.n = (int)n;
-  a.L = L;
+  FwdArgs a = forward_args(in, (int)n, K, cb, L, temp_edges, temp_costs);
   a.roll = roll;
-  a.store_rows = L;
-  a.cb = cb;
   a.pre_states = pre_states;
   a.pre_stride = 1;
-  a.bp = temp_edges;
-  a.bp_tile_stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
-  a.term_costs = temp_costs;
   a.cost_slot = cost_slot;
-  a.best_edges = nullptr;
   return launch_forward(a, K, generic, as_stream(stream));
 }
 
@@ -682,19 +916,22 @@ int exl3_backward_pass(const uint16_t* temp_costs, const uint8_t* temp_edges, fl
   if (roll < 0 || roll >= L) return set_error("roll must be in [0, L), got %d", roll);
   if (!temp_costs || !temp_edges || !end_states) return set_error("NULL buffer");
   if (write && (!out_w || !out_idx)) return set_error("NULL output buffer");
-  const BpLayout lay = layout_for(K);
-  const int64_t stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
   hipStream_t st = as_stream(stream);
+  TbArgs t = traceback_args(temp_edges, (int)n, K, cb, L, roll, write);
+  t.start = end_states;
+  t.start_stride = 1;
   if (!write) {
     const int E = 65536 >> K;
     hipLaunchKernelGGL(argmin_costs_kernel, dim3((unsigned)n), dim3(256), 0, st, temp_costs, E,
                        cost_slot, end_states);
     if (check_launch("argmin_costs")) return 1;
-    return launch_traceback(temp_edges, stride, lay, (int)n, L, roll, 0, end_states, 1,
-                            end_states, 1, nullptr, nullptr, cb, st);
+    t.end_out = end_states;
+    t.end_stride = 1;
+  } else {
+    t.out_w = out_w;
+    t.out_idx = out_idx;
   }
-  return launch_traceback(temp_edges, stride, lay, (int)n, L, roll, 1, end_states, 1, nullptr, 1,
-                          out_w, out_idx, cb, st);
+  return launch_traceback(t, st);
 }
 
 int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_t* temp_costs,
@@ -706,48 +943,48 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
   if (!in || !out_w || !out_idx || !temp_costs || !temp_edges) return set_error("NULL buffer");
   const BpLayout lay = layout_for(K);
   const int64_t stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
-  // Header row of each tile: int32 {pass-1 terminal edge, end state}.
-  const int64_t hdr = (int64_t)L * lay.row_bytes;
+  // Header row of each tile: int32 {pass-1 terminal edge, end state, ...}.
   const int64_t hstride = stride / 4;
-  int32_t* best_edges = reinterpret_cast<int32_t*>(temp_edges + hdr);
-  int32_t* end_states = best_edges + 1;
+  int32_t* hdr = reinterpret_cast<int32_t*>(temp_edges + (int64_t)L * lay.row_bytes);
+  int32_t* best_edges = hdr + exl3::HDR_BEST_EDGE;
+  int32_t* end_states = hdr + exl3::HDR_END_STATE;
   const int64_t cap = (wave_cap > 0) ? std::min(batch_cap, wave_cap) : batch_cap;
   const int64_t chunk_max = std::min<int64_t>(cap, INT32_MAX);
   hipStream_t st = as_stream(stream);
 
   for (int64_t off = 0; off < n; off += chunk_max) {
     const int chunk = (int)std::min<int64_t>(chunk_max, n - off);
-    FwdArgs a{};
-    a.in = in + off * L;
-    a.n = chunk;
-    a.L = L;
-    a.cb = cb;
-    a.bp = temp_edges;
-    a.bp_tile_stride = stride;
-    a.term_costs = temp_costs;
-    // Pass 1: rotation L/2, unconstrained; only ring rows 0..L/2-1 are read
-    // back (reference_encoder.py:284-288).
+    FwdArgs a = forward_args(in + off * L, chunk, K, cb, L, temp_edges, temp_costs);
+    // Pass 1: rotation L/2, unconstrained. The traceback reads ring rows
+    // 0..L/2-1 only, i.e. forward steps L/2..L-1 (reference_encoder.py:284-288).
     a.roll = L / 2;
     a.store_rows = L / 2;
-    a.pre_states = nullptr;
+    a.store_from = L / 2 - 1;
     a.cost_slot = 0;
     a.best_edges = best_edges;
     a.best_stride = hstride;
     if (launch_forward(a, K, generic, st)) return 1;
-    if (launch_traceback(temp_edges, stride, lay, chunk, L, L / 2, 0, best_edges, hstride,
-                         end_states, hstride, nullptr, nullptr, cb, st))
-      return 1;
+    TbArgs t1 = traceback_args(temp_edges, chunk, K, cb, L, L / 2, 0);
+    t1.start = best_edges;
+    t1.start_stride = hstride;
+    t1.end_out = end_states;
+    t1.end_stride = hstride;
+    if (launch_traceback(t1, st)) return 1;
     // Pass 2: natural order, wrap constrained to the end state (:290-293).
     a.roll = 0;
     a.store_rows = L;
+    a.store_from = 0;
     a.pre_states = end_states;
     a.pre_stride = hstride;
     a.cost_slot = 1;
     a.best_edges = nullptr;
     if (launch_forward(a, K, generic, st)) return 1;
-    if (launch_traceback(temp_edges, stride, lay, chunk, L, 0, 1, end_states, hstride, nullptr,
-                         1, out_w + off * L, out_idx + off * L, cb, st))
-      return 1;
+    TbArgs t2 = traceback_args(temp_edges, chunk, K, cb, L, 0, 1);
+    t2.start = end_states;
+    t2.start_stride = hstride;
+    t2.out_w = out_w + off * L;
+    t2.out_idx = out_idx + off * L;
+    if (launch_traceback(t2, st)) return 1;
   }
   return 0;
 }

@@ -1,5 +1,5 @@
-// Trellis geometry and backpointer layout shared by the HIP kernels and the
-// host side of the C-ABI.
+// Trellis geometry and per-tile scratch layout shared by the HIP kernels and
+// the host side of the C-ABI.
 //
 // Trellis (reference: exl3_quant/reference_encoder.py:89-113,
 // docs/algorithm_contract.md:199-213). A 16-bit state sigma at bitrate K is
@@ -8,20 +8,30 @@
 // Writing e = (h << K) | j with group h in [0, S), S = 2^(16-2K), and
 // j in [0, 2^K), the predecessor is (k << (16-2K)) | h: all 2^K edges of
 // group h read the same 2^K predecessor costs. That 2^K x 2^K block is the
-// unit of work the fast kernel assigns to threads.
+// unit of work the fast kernels assign to threads.
 //
-// Backpointers. The reference stores the full predecessor edge as int16 per
-// (ring row, edge) (quantize_kernels.sycl:124,153). Here only the winning
-// branch k is stored, in BPB bits per edge (BPB = K rounded up to 1, 2, 4 or
-// 8 so that fields never straddle a byte boundary), since the predecessor
-// is (k << (16-2K)) | (e >> K). Inside a row the fields are stored in
-// "slot" order: the fast kernel's thread `unit` owns EPT = G*J consecutive
-// slots, so each thread writes its bits for a step with one 16- or 32-bit
-// store. bp_slot() maps an edge to its slot.
+// The reference keeps, per (ring row, edge), the chosen predecessor edge as
+// int16 (quantize_kernels.sycl:124,153). Here the per-tile scratch holds one
+// of two things, chosen by K:
 //
-// Per-tile scratch block: (L + 1) rows of ROWB = E*BPB/8 bytes. Rows 0..L-1
-// hold the backpointers of ring rows 0..L-1; row L is a header holding
-// int32 {pass-1 terminal edge, end state} for the fused encoder.
+// * backpointer rows (K = 1, 2, 8): only the winning branch k, in BPB bits
+//   per edge (K rounded up to 1, 2, 4 or 8), since the predecessor is
+//   (k << (16-2K)) | (e >> K). Inside a row the fields are in "slot" order:
+//   the fast kernel's thread `unit` owns G*J consecutive slots and writes
+//   them with one 32-bit store per step; bp_slot() maps an edge to its slot.
+//   Row r holds ring row r.
+// * cost rows (K = 3..7): the fp16 path-cost vector after each step
+//   (E * 2 bytes, edge order). The forward pass then only needs the minimum
+//   cost per edge, which packed fp16 arithmetic computes at the VALU roofline,
+//   and the traceback recomputes the 2^K candidates of the one edge on the
+//   path from row i-1 (the costs the forward step i read). Row i holds the
+//   output of trellis step i (step order, independent of the ring roll).
+//   For K <= 2 these rows would outweigh the HBM budget (32-64 KiB/step).
+//
+// Per-tile block: (L + 1) rows of row_bytes. Row L is a header:
+//   int32 [0] pass-1 terminal edge, [1] end state, [2] pre_state of the last
+//   forward pass; from byte 16, L fp16 inputs in ring order (cost-row mode),
+//   which the traceback reads.
 #pragma once
 
 #include <stdint.h>
@@ -34,61 +44,65 @@
 
 namespace exl3 {
 
+enum { MODE_BACKPOINTERS = 0, MODE_COST_ROWS = 1 };
+
 struct BpLayout {
   int32_t K;        // bitrate
-  int32_t G;        // groups per thread (fast layout)
-  int32_t J;        // edges per group per thread (fast layout)
-  int32_t BPB;      // bits per backpointer field
-  int32_t natural;  // 1: slot == edge (K = 8)
+  int32_t mode;     // MODE_BACKPOINTERS or MODE_COST_ROWS
+  int32_t G;        // groups per thread (backpointer slot order)
+  int32_t J;        // edges per group per thread (backpointer slot order)
+  int32_t BPB;      // bits per field (16 in cost-row mode)
+  int32_t natural;  // 1: slot == edge
   int32_t row_bytes;
 };
+
+EXL3_HD inline bool uses_cost_rows(int K) { return K >= 3 && K <= 7; }
 
 EXL3_HD inline int32_t bits_per_backpointer(int K) {
   return K == 3 ? 4 : (K >= 5 ? 8 : K);
 }
 
-// Thread decomposition of the fast forward kernel for each K (all use 1024
-// threads and 64 candidate branches per thread per step):
-//   K : G  J  P
-//   1 : 16 2  1
-//   2 :  4 4  1
-//   3 :  4 2  1
-//   4 :  4 1  1
-//   5 :  2 1  1
-//   6 :  2 1  2
-//   7 :  2 1  4
-// K = 8 has a single group and runs on the generic kernel.
+// Thread decomposition of the fast forward kernels for each K (all use 1024
+// threads and 64 candidate branches per thread per step; P lanes split the
+// 2^K branches of one edge set, Q = 2^K / P per lane):
+//   K : G  J  P   Q   scratch
+//   1 : 16 2  1   2   backpointers (key kernel)
+//   2 :  4 4  1   4   backpointers (key kernel)
+//   3 :  4 2  1   8   cost rows (row kernel)
+//   4 :  4 1  1  16   cost rows
+//   5 :  2 1  1  32   cost rows
+//   6 :  2 1  2  32   cost rows
+//   7 :  2 1  4  32   cost rows
+// K = 8 has a single group and runs on the generic kernel. Must match
+// FastShape in exl3_encoder.hip.
 EXL3_HD inline int fast_G(int K) { return K == 1 ? 16 : (K <= 4 ? 4 : 2); }
 EXL3_HD inline int fast_J(int K) { return K == 1 ? 2 : (K == 2 ? 4 : (K == 3 ? 2 : 1)); }
 EXL3_HD inline int fast_P(int K) { return K == 6 ? 2 : (K == 7 ? 4 : 1); }
 EXL3_HD inline bool has_fast_kernel(int K) { return K >= 1 && K <= 7; }
 
-// Backpointer layout of bitrate K. It depends on K only: the generic kernel
-// writes the same layout as the fast kernel, so the split forward/backward
-// passes may mix kernel variants. K = 8 (no fast kernel) uses one byte per
-// edge in edge order.
+// Scratch layout of bitrate K (the same for every kernel variant, so the
+// split forward/backward passes may mix them).
 EXL3_HD inline BpLayout make_layout(int K) {
   BpLayout l;
   l.K = K;
   const int E = 65536 >> K;
-  if (!has_fast_kernel(K)) {
-    l.G = 1;
-    l.J = 1;
-    l.BPB = 8;
-    l.natural = 1;
+  l.mode = uses_cost_rows(K) ? MODE_COST_ROWS : MODE_BACKPOINTERS;
+  l.G = fast_G(K);
+  l.J = fast_J(K);
+  l.natural = (K == 8) ? 1 : 0;
+  if (l.mode == MODE_COST_ROWS) {
+    l.BPB = 16;
+    l.row_bytes = E * 2;
   } else {
-    l.G = fast_G(K);
-    l.J = fast_J(K);
-    l.BPB = bits_per_backpointer(K);
-    l.natural = 0;
+    l.BPB = (K == 8) ? 8 : bits_per_backpointer(K);
+    l.row_bytes = E * l.BPB / 8;
   }
-  l.row_bytes = E * l.BPB / 8;
   return l;
 }
 
-// Slot of edge e inside a backpointer row.
+// Slot of edge e inside a backpointer row (edge order in cost-row mode).
 EXL3_HD inline uint32_t bp_slot(const BpLayout& l, uint32_t e) {
-  if (l.natural) return e;
+  if (l.natural || l.mode == MODE_COST_ROWS) return e;
   const uint32_t h = e >> l.K;
   const uint32_t j = e & ((1u << l.K) - 1u);
   const uint32_t G = (uint32_t)l.G, J = (uint32_t)l.J;
@@ -102,5 +116,11 @@ EXL3_HD inline uint32_t bp_slot(const BpLayout& l, uint32_t e) {
 EXL3_HD inline uint64_t tile_scratch_bytes(const BpLayout& l, int L) {
   return (uint64_t)(L + 1) * (uint64_t)l.row_bytes;
 }
+
+// Header row fields (row L of each tile block).
+constexpr int HDR_BEST_EDGE = 0;  // int32 index
+constexpr int HDR_END_STATE = 1;  // int32 index
+constexpr int HDR_PRE_STATE = 2;  // int32 index
+constexpr int HDR_W_BYTES = 16;   // byte offset of the L fp16 inputs (cost-row mode)
 
 }  // namespace exl3

@@ -14,10 +14,11 @@ is no CPU fallback.
 
 Deviations from the reference, all deliberate:
 
-* scratch layout: ``temp_edges`` is ``uint8 (B, L+1, ROWB)`` K-bit
-  backpointers (include/exl3_encoder.h), sized by the new ScratchEstimator;
-* the arena's default batch capacity is 8192 tiles (the reference used 64 for
-  the Arc iGPU), enough for several waves of 1024-thread workgroups on 256 CUs;
+* scratch layout: ``temp_edges`` is ``uint8 (B, L+1, ROW)``: K-bit
+  backpointer rows (K = 1, 2, 8) or fp16 cost rows (K = 3..7), see
+  include/exl3_encoder.h; sized by the new ScratchEstimator;
+* the arena's default batch capacity is 4096 tiles (the reference used 64 for
+  the Arc iGPU), enough for eight waves of 1024-thread workgroups on 256 CUs;
 * traceback placement: ``gpu_resident`` runs the fused encoder;
   ``gpu_resident_split``, ``d2h_cpu`` and ``usm_host`` run the split
   forward/traceback passes on the GPU (the host modes existed to work around
@@ -132,7 +133,7 @@ class ScratchArena:
     it; a failed admission or allocation halves B down to 1."""
 
     def __init__(self, policy: Optional[MemoryPolicy] = None, device_index: int = 0,
-                 default_cap_b: int = 8192):
+                 default_cap_b: int = 4096):
         self.policy = policy or MemoryPolicy()
         self.device_index = device_index
         self.default_cap_b = default_cap_b

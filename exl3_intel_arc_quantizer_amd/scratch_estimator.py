@@ -1,18 +1,20 @@
-"""Scratch sizing for the MI355X encoder (K-bit backpointer layout).
+"""Scratch sizing for the MI355X encoder (K-bit backpointer / cost-row layout).
 
 Counterpart of exl3_quant/scratch_estimator.py:23-172 with the same class
 and method names. The formula changes with the layout
 (include/exl3_encoder.h):
 
     S      = 65536 >> K                      edges per step
-    BPB    = K rounded up to 1, 2, 4 or 8    bits per backpointer
+    row    = S * BPB / 8                     K = 1, 2, 8: K-bit backpointer rows
+                                             (BPB = K rounded up to 1, 2, 4, 8)
+           = S * 2                           K = 3..7: fp16 cost rows
     costs  = B * 2 * S * 2                   terminal fp16 costs of both passes
-    edges  = B * (T + 1) * S * BPB / 8       K-bit backpointer rows + header row
+    edges  = B * (T + 1) * row               T rows + one header row per tile
 
 The reference's int16 layout, ``B * T * S * 2``, is still available by
 passing ``bytes_per_edge`` explicitly (e.g. to compare the two). Per tile at
-T = 256: K=2 1.0 MiB (reference 8 MiB), K=4 514 KiB (2 MiB), K=6 257 KiB
-(512 KiB).
+T = 256: K=2 1.0 MiB (reference 8 MiB), K=3 4.0 MiB (4 MiB), K=4 2.0 MiB
+(2 MiB), K=6 514 KiB (512 KiB).
 """
 
 from __future__ import annotations
@@ -29,13 +31,20 @@ BYTES_PER_MB = 1000 ** 2
 BYTES_PER_GB = 1000 ** 3
 
 
+def uses_cost_rows(k: int) -> bool:
+    """K = 3..7 keep fp16 cost rows; K = 1, 2, 8 keep K-bit backpointers."""
+    return 3 <= k <= 7
+
+
 def backpointer_bits(k: int) -> int:
-    """Bits stored per backpointer field (exl3_layout.h bits_per_backpointer)."""
-    return 4 if k == 3 else (8 if k >= 5 else k)
+    """Bits stored per edge and row (exl3_layout.h make_layout)."""
+    if uses_cost_rows(k):
+        return 16
+    return 8 if k == 8 else k
 
 
 def backpointer_row_bytes(k: int) -> int:
-    """Bytes of one backpointer row (exl3_scratch_row_bytes)."""
+    """Bytes of one scratch row (exl3_scratch_row_bytes)."""
     return (65536 >> k) * backpointer_bits(k) // 8
 
 

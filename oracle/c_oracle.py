@@ -51,7 +51,8 @@ def lib():
                                          ctypes.c_int]
         L.exl3o_encode_tiles.restype = ctypes.c_int
         L.exl3o_forward_pass.argtypes = [_u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                         ctypes.c_int, ctypes.c_int, _u16p, _u16p]
+                                         ctypes.c_int, ctypes.c_int, _u16p, _u16p,
+                                         ctypes.c_void_p]
         L.exl3o_forward_pass.restype = ctypes.c_int
         L.exl3o_pack_tiles.argtypes = [_u16p, ctypes.c_int64, ctypes.c_int, _u16p]
         L.exl3o_pack_tiles.restype = None
@@ -85,16 +86,22 @@ def fma_f16(dh: np.ndarray, cost: np.ndarray) -> np.ndarray:
     return out.view(np.float16)
 
 
-def forward_pass(tile16: np.ndarray, K: int, cb: int, roll: int, pre_state: int):
-    """One forward pass: returns (edges (L, E) uint16, terminal costs fp16)."""
+def forward_pass(tile16: np.ndarray, K: int, cb: int, roll: int, pre_state: int,
+                 with_rows: bool = False):
+    """One forward pass: returns (edges (L, E) uint16, terminal costs fp16) and,
+    with ``with_rows``, the cost vector after every step (L, E) fp16 bits."""
     t = np.ascontiguousarray(tile16, dtype=np.float16).view(np.uint16)
     L = t.size
     E = 65536 >> K
     edges = np.empty((L, E), dtype=np.uint16)
     costs = np.empty(E, dtype=np.uint16)
-    rc = lib().exl3o_forward_pass(t, K, cb, L, roll, pre_state, edges, costs)
+    rows = np.empty((L, E), dtype=np.uint16) if with_rows else None
+    rc = lib().exl3o_forward_pass(t, K, cb, L, roll, pre_state, edges, costs,
+                                  rows.ctypes.data if with_rows else None)
     if rc != 0:
         raise RuntimeError(f"exl3o_forward_pass failed ({rc})")
+    if with_rows:
+        return edges, costs.view(np.float16), rows
     return edges, costs.view(np.float16)
 
 

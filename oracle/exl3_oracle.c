@@ -139,7 +139,7 @@ static inline int ring_index(int i, int roll, int L) {
  * cost_out. lut: fp16 bits of every state. */
 static void forward_pass(const uint16_t* lut, const uint16_t* tile16, int K, int L, int roll,
                          int pre_state, uint16_t* edges, uint16_t* cost_a, uint16_t* cost_b,
-                         uint16_t** cost_out) {
+                         uint16_t** cost_out, uint16_t* rows) {
   const int E = 65536 >> K, Kr = 16 - K, Q = 1 << K;
   uint16_t* prev = cost_a;
   uint16_t* next = cost_b;
@@ -168,6 +168,7 @@ static void forward_pass(const uint16_t* lut, const uint16_t* tile16, int K, int
       next[e] = best;
       row[e] = best_pred;
     }
+    if (rows) memcpy(rows + (size_t)i * E, next, (size_t)E * sizeof(uint16_t));
     uint16_t* t = prev;
     prev = next;
     next = t;
@@ -206,7 +207,7 @@ static void encode_one(const uint16_t* lut, const uint16_t* tile16, int K, int L
                        uint16_t* ca, uint16_t* cb_, tile_out_t o) {
   const int E = 65536 >> K;
   uint16_t* c1;
-  forward_pass(lut, tile16, K, L, L / 2, -1, edges, ca, cb_, &c1);
+  forward_pass(lut, tile16, K, L, L / 2, -1, edges, ca, cb_, &c1, NULL);
   const int best = argmin_cost(c1, E);
   /* backward(write=False): reference_encoder.py:239-249 */
   int edge = best;
@@ -217,7 +218,7 @@ static void encode_one(const uint16_t* lut, const uint16_t* tile16, int K, int L
   }
   const int end_state = edge;
   uint16_t* c2;
-  forward_pass(lut, tile16, K, L, 0, end_state, edges, ca, cb_, &c2);
+  forward_pass(lut, tile16, K, L, 0, end_state, edges, ca, cb_, &c2, NULL);
   edge = end_state;
   for (int i = L - 1; i >= 0; --i) {
     const int prev = edges[(size_t)i * E + edge];
@@ -273,9 +274,11 @@ ORACLE_API int exl3o_encode_tiles(const uint16_t* tiles16, int64_t n, int K, int
 }
 
 /* One forward pass on one tile, exposing the full predecessor table
- * (reference_encoder.py:130-204); used to pin forward() on its own. */
+ * (reference_encoder.py:130-204) and, when rows is not NULL, the cost vector
+ * after every step (rows[i*E + e]); used to pin forward() on its own. */
 ORACLE_API int exl3o_forward_pass(const uint16_t* tile16, int K, int cb, int L, int roll,
-                                  int pre_state, uint16_t* edges, uint16_t* costs_out) {
+                                  int pre_state, uint16_t* edges, uint16_t* costs_out,
+                                  uint16_t* rows) {
   if (K < 1 || K > 8 || cb < 0 || cb > 2 || L <= 0 || (L & 1)) return -1;
   init_tables();
   const int E = 65536 >> K;
@@ -288,7 +291,7 @@ ORACLE_API int exl3o_forward_pass(const uint16_t* tile16, int K, int cb, int L, 
   }
   exl3o_codebook_lut(cb, lut);
   uint16_t* out;
-  forward_pass(lut, tile16, K, L, roll, pre_state, edges, ca, cbuf, &out);
+  forward_pass(lut, tile16, K, L, roll, pre_state, edges, ca, cbuf, &out, rows);
   memcpy(costs_out, out, (size_t)E * sizeof(uint16_t));
   free(lut); free(ca); free(cbuf);
   return 0;

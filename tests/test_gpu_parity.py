@@ -162,17 +162,22 @@ def _pred_table(temp_edges_row_block, K, L):
 @pytest.mark.parametrize("generic", [False, True])
 def test_forward_pass_pins(ext, torch_mod, generic):
     """Split forward pass (quantize_xpu.cpp:169-215) against the reference's
-    forward(): terminal costs bit-exact and the full predecessor table hash."""
+    forward(): terminal costs bit-exact; in backpointer mode (K = 1, 2, 8) the
+    full predecessor table against its hash; in cost-row mode (K = 3..7) every
+    stored cost row against the C oracle's per-step costs. Then the split
+    backward pass reaches the reference's end state."""
     from exl3_intel_arc_quantizer_amd._native import row_bytes
+    from exl3_intel_arc_quantizer_amd.scratch_estimator import uses_cost_rows
     g = load_golden("forward_pass")
     for i in range(4):
         K, roll, pre, best, end = (int(v) for v in g[f"case{i}_meta"])
         print(f"forward case {i}: K={K} roll={roll} pre={pre} generic={generic}", flush=True)
-        x = torch_mod.from_numpy(g[f"case{i}_tile"].view(np.float16).astype(np.float32)).cuda()
-        x = x.reshape(1, 256)
+        tile16 = g[f"case{i}_tile"].view(np.float16)
+        x = torch_mod.from_numpy(tile16.astype(np.float32)).cuda().reshape(1, 256)
         E = 65536 >> K
+        rb = row_bytes(K)
         costs = torch_mod.zeros((1, 2, E), dtype=torch_mod.float16, device="cuda")
-        edges = torch_mod.zeros((1, 257, row_bytes(K)), dtype=torch_mod.uint8, device="cuda")
+        edges = torch_mod.zeros((1, 257, rb), dtype=torch_mod.uint8, device="cuda")
         pre_t = torch_mod.full((1,), pre, dtype=torch_mod.int32, device="cuda")
         ext.quantize_tiles_forward_pass(x, costs, edges, pre_t, K, False, True, roll, 1, 32,
                                         generic)
@@ -184,9 +189,19 @@ def test_forward_pass_pins(ext, torch_mod, generic):
         torch_mod.cuda.synchronize()
         np.testing.assert_array_equal(costs[0, 1].cpu().numpy().view(np.uint16),
                                       g[f"case{i}_costs"])
-        table = _pred_table(edges[0].cpu().numpy(), K, 256)
-        np.testing.assert_array_equal(table[:4, :64], g[f"case{i}_edges_head"])
-        assert hashlib.sha256(table.tobytes()).hexdigest() == str(g[f"case{i}_edges_sha256"])
+        block = edges[0].cpu().numpy()
+        if uses_cost_rows(K):
+            _, _, want_rows = c_oracle.forward_pass(tile16, K=K, cb=2, roll=roll, pre_state=pre,
+                                                    with_rows=True)
+            got_rows = block[:255].view(np.uint16).reshape(255, E)
+            np.testing.assert_array_equal(got_rows, want_rows[:255])
+            hdr = block[256]
+            np.testing.assert_array_equal(hdr[16:16 + 512].view(np.uint16), tile16.view(np.uint16))
+            assert int(hdr[8:12].view(np.int32)[0]) == pre
+        else:
+            table = _pred_table(block, K, 256)
+            np.testing.assert_array_equal(table[:4, :64], g[f"case{i}_edges_head"])
+            assert hashlib.sha256(table.tobytes()).hexdigest() == str(g[f"case{i}_edges_sha256"])
         assert int(ends.item()) == end
 
 

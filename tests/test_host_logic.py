@@ -29,9 +29,9 @@ def test_reference_formula_fixtures_still_reproducible():
         assert a.costs_mib == pytest.approx(costs_mib)
 
 
-@pytest.mark.parametrize("k,per_tile", [(1, 257 * 4096), (2, 257 * 4096), (3, 257 * 4096),
-                                        (4, 257 * 2048), (5, 257 * 2048), (6, 257 * 1024),
-                                        (7, 257 * 512), (8, 257 * 256)])
+@pytest.mark.parametrize("k,per_tile", [(1, 257 * 4096), (2, 257 * 4096), (3, 257 * 16384),
+                                        (4, 257 * 8192), (5, 257 * 4096), (6, 257 * 2048),
+                                        (7, 257 * 1024), (8, 257 * 256)])
 def test_kbit_layout_formula(k, per_tile):
     a = ScratchEstimator.estimate_scratch(k=k, t=256, b=10)
     assert a.edges_bytes == 10 * per_tile
@@ -54,7 +54,7 @@ def test_estimator_validation_and_max_batch():
     assert max_b == (288 * 10 ** 9 - 8 * BYTES_PER_GIB) // (257 * 4096 + 2 * 16384 * 2)
     max_b, _ = ScratchEstimator.calculate_max_batch_size(
         k=3, available_vram_bytes=64 * BYTES_PER_GIB, max_single_alloc_bytes=16 * BYTES_PER_MIB)
-    assert max_b == 16 * BYTES_PER_MIB // (257 * 4096)
+    assert max_b == 16 * BYTES_PER_MIB // (257 * 16384)
     with pytest.raises(ValueError):
         ScratchEstimator.calculate_max_batch_size(k=2, available_vram_bytes=BYTES_PER_GIB)
 
