@@ -96,6 +96,15 @@ def time_steps(batch, steps, warmup, torch):
     return (time.perf_counter() - t0) / steps
 
 
+def forward_kernel_name(K):
+    """The forward kernel the fast path launches for bitrate K."""
+    if K in (1, 2):
+        return f"acs_forward_tourn<K={K}>"
+    if 3 <= K <= 7:
+        return f"acs_forward_rows<K={K}>"
+    return "acs_forward_generic"
+
+
 def forward_kernel_roofline(batch, torch, reps=3):
     """Mean duration of one forward-pass launch over the whole batch, timed
     with HIP events recorded on the launch stream."""
@@ -116,7 +125,7 @@ def forward_kernel_roofline(batch, torch, reps=3):
     return {"bound": "valu", "achieved": round(achieved / 1e12, 3),
             "peak": round(PEAK_ELEM_OPS / 1e12, 3), "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_ELEM_OPS, 4), "traffic": None,
-            "kernel": f"acs_forward_fast<K={batch.K}>", "launch_ms": round(ms, 3),
+            "kernel": forward_kernel_name(batch.K), "launch_ms": round(ms, 3),
             "tiles_per_launch": n,
             "ops_note": "fp16 element-ops: tiles*256 steps*65536 candidates*3 (sub, FMA, "
                         "compare-select); peak 256 CU*64 lanes*2 halves*2.4 GHz"}

@@ -13,10 +13,10 @@
 //                      per edge only. Each step's cost row goes to HBM with
 //                      coalesced 16-byte stores; the traceback recomputes the
 //                      argmin of the one edge on the path.
-//   acs_forward_keys   K = 1, 2 (cost rows would cost 32-64 KiB per step):
-//                      the first minimum over branches is an unsigned min over
-//                      32-bit keys (cost bits << 16 | branch); winning branches
-//                      leave as K-bit backpointers.
+//   acs_forward_tourn  K = 1, 2 (cost rows would cost 32-64 KiB per step):
+//                      the first minimum over branches by a packed knockout
+//                      (v_pk_min_u16 + the sign of v_pk_sub_i16 per match);
+//                      winning branches leave as K-bit backpointers.
 //   acs_forward_generic reference-structured kernel (one edge per thread
 //                      iteration, codebook decoded per candidate, strict fp16
 //                      '<' scan): K = 8 and the force_global_costs variant;
@@ -366,26 +366,53 @@ __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
   forward_epilogue<C::NT>(a, C::E, s_cost[L & 1], s_red);
 }
 
-// Key forward pass (K = 1, 2): first minimum over branches with K-bit
-// backpointers in slot order.
-template <int K, int G, int J, int P, int CB>
-__global__ void __launch_bounds__(1024) acs_forward_keys(FwdArgs a) {
+// Tournament forward pass (K = 1, 2): first minimum over the 2^K branches by
+// a packed knockout. For a register pair E_q = [cost of edge b | edge a] at
+// branch q, a match of q0 < q1 keeps min(E_q0, E_q1) (v_pk_min_u16) and
+// records q1 as the winner only when E_q1 < E_q0 strictly: the sign bit of
+// v_pk_sub_i16 (exact since costs lie in [0, 0x7C00]). The lower branch wins
+// ties, so the final winner is the reference's first minimum.
+// The winners' bits sit at bits 15 and 31 of each difference word; v_perm
+// gathers the bytes holding them for two register pairs into one word (bit
+// 7 of each byte), and a byte-wise shift register (shift right by one,
+// insert at bit 7) stacks eight such words into the thread's 32-bit
+// backpointer word, in bp_slot order.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t bfi32(uint32_t mask, uint32_t a, uint32_t b) {
+  return (mask & a) | (~mask & b);
+}
+
+// Bytes 1 and 3 of `lo_pair` (its sign bits), then bytes 1 and 3 of `hi_pair`.
+__device__ __forceinline__ uint32_t gather_signs(uint32_t lo_pair, uint32_t hi_pair) {
+  return __builtin_amdgcn_perm(lo_pair, hi_pair, 0x03010705u);
+}
+
+__device__ __forceinline__ uint32_t push_signs(uint32_t acc, uint32_t signs) {
+  return bfi32(0x80808080u, signs, acc >> 1);
+}
+
+template <int K, int G, int J, int CB>
+__global__ void __launch_bounds__(1024) acs_forward_tourn(FwdArgs a) {
+  constexpr int P = 1;
   using C = FastCfg<K, G, J, P>;
-  static_assert(C::UNIT_BITS == 16 || C::UNIT_BITS == 32, "unit store width");
+  static_assert(K == 1 || K == 2, "tournament kernel handles 2 or 4 branches");
+  static_assert(G * J * K == 32, "one 32-bit backpointer word per thread and step");
+  constexpr int PAIRS = (G / 2) * J;
+  static_assert(PAIRS * K == 16, "eight sign words per backpointer word");
   __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][C::E];
   __shared__ f16 s_w[256];
   __shared__ uint32_t s_red[16];
 
   const int L = a.L;
   const int tid = threadIdx.x;
-  const int p = tid % P;
-  const int unit = tid / P;
+  const int unit = tid;
   const int jj = unit % C::NJ;
   const int gq = unit / C::NJ;
   const int h0 = gq * G;
 
   f16x2 cbv[G / 2][J][C::Q];
-  load_codebook<K, G, J, C::Q, C::KR, CB>(cbv, p, jj, h0);
+  load_codebook<K, G, J, C::Q, C::KR, CB>(cbv, 0, jj, h0);
   int pre;
   forward_prologue<C::NT>(a, C::E, false, s_w, s_cost[0], pre);
   __syncthreads();
@@ -401,51 +428,56 @@ __global__ void __launch_bounds__(1024) acs_forward_keys(FwdArgs a) {
     w2.x = w;
     w2.y = w;
 
-    uint32_t best[G / 2][J][2];
-#pragma unroll
-    for (int g2 = 0; g2 < G / 2; ++g2)
-#pragma unroll
-      for (int jl = 0; jl < J; ++jl) best[g2][jl][0] = best[g2][jl][1] = 0xFFFFFFFFu;
-
+    uint32_t cpair[C::Q][G / 2];
 #pragma unroll
     for (int q = 0; q < C::Q; ++q) {
-      const uint32_t k = (uint32_t)(p * C::Q + q);
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(cin + k * C::S + h0);
-      uint32_t cpair[G / 2];
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(cin + q * C::S + h0);
 #pragma unroll
-      for (int g2 = 0; g2 < G / 2; ++g2) cpair[g2] = src[g2];
-#pragma unroll
-      for (int g2 = 0; g2 < G / 2; ++g2)
-#pragma unroll
-        for (int jl = 0; jl < J; ++jl) {
-          const f16x2 dh = cbv[g2][jl][q] - w2;
-          const f16x2 err =
-              __builtin_elementwise_fma(dh, dh, __builtin_bit_cast(f16x2, cpair[g2]));
-          const uint32_t eb = __builtin_bit_cast(uint32_t, err);
-          best[g2][jl][0] = umin(best[g2][jl][0], (eb << 16) | k);
-          best[g2][jl][1] = umin(best[g2][jl][1], (eb & 0xFFFF0000u) | k);
-        }
+      for (int g2 = 0; g2 < G / 2; ++g2) cpair[q][g2] = src[g2];
     }
 
-    uint32_t bits = 0;
+    uint32_t acc = 0;
 #pragma unroll
-    for (int g2 = 0; g2 < G / 2; ++g2)
+    for (int pp0 = 0; pp0 < PAIRS; pp0 += 2) {
+      uint32_t lo_bit[2], hi_bit[2];  // sign words: branch bit 0 and (K = 2) bit 1
 #pragma unroll
-      for (int jl = 0; jl < J; ++jl)
+      for (int u = 0; u < 2; ++u) {
+        const int g2 = (pp0 + u) / J;
+        const int jl = (pp0 + u) % J;
+        u16x2 e[C::Q];
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const uint32_t key = quad_min<P>(best[g2][jl][half]);
-          const int e = ((h0 + 2 * g2 + half) << K) | (jj * J + jl);
-          if (P == 1 || p == 0) cout[e] = (uint16_t)(key >> 16);
-          bits |= (key & 0xFFFFu) << (((g2 * J + jl) * 2 + half) * C::BPB);
+        for (int q = 0; q < C::Q; ++q) {
+          const f16x2 dh = cbv[g2][jl][q] - w2;
+          e[q] = __builtin_bit_cast(
+              u16x2, __builtin_elementwise_fma(dh, dh, __builtin_bit_cast(f16x2, cpair[q][g2])));
         }
-    if (ri < a.store_rows && (P == 1 || p == 0)) {
-      uint8_t* row = tile_bp + (int64_t)ri * C::ROWB;
-      if (C::UNIT_BITS == 32)
-        reinterpret_cast<uint32_t*>(row)[unit] = bits;
-      else
-        reinterpret_cast<uint16_t*>(row)[unit] = (uint16_t)bits;
+        u16x2 m;
+        if constexpr (K == 1) {
+          m = __builtin_elementwise_min(e[0], e[1]);
+          lo_bit[u] = __builtin_bit_cast(
+              uint32_t, __builtin_bit_cast(s16x2, e[1]) - __builtin_bit_cast(s16x2, e[0]));
+          hi_bit[u] = 0;
+        } else {
+          const u16x2 m01 = __builtin_elementwise_min(e[0], e[1]);
+          const u16x2 m23 = __builtin_elementwise_min(e[2], e[3]);
+          m = __builtin_elementwise_min(m01, m23);
+          const uint32_t d01 = __builtin_bit_cast(
+              uint32_t, __builtin_bit_cast(s16x2, e[1]) - __builtin_bit_cast(s16x2, e[0]));
+          const uint32_t d23 = __builtin_bit_cast(
+              uint32_t, __builtin_bit_cast(s16x2, e[3]) - __builtin_bit_cast(s16x2, e[2]));
+          const uint32_t dr = __builtin_bit_cast(
+              uint32_t, __builtin_bit_cast(s16x2, m23) - __builtin_bit_cast(s16x2, m01));
+          hi_bit[u] = dr;
+          lo_bit[u] = bfi32(dr, d23, d01);  // the winning side's first match
+        }
+        const int ea = ((h0 + 2 * g2) << K) | (jj * J + jl);
+        cout[ea] = m.x;
+        cout[ea + (1 << K)] = m.y;
+      }
+      acc = push_signs(acc, gather_signs(lo_bit[0], lo_bit[1]));
+      if constexpr (K == 2) acc = push_signs(acc, gather_signs(hi_bit[0], hi_bit[1]));
     }
+    if (ri < a.store_rows) reinterpret_cast<uint32_t*>(tile_bp + (int64_t)ri * C::ROWB)[unit] = acc;
     __syncthreads();
   }
   forward_epilogue<C::NT>(a, C::E, s_cost[L & 1], s_red);
@@ -777,8 +809,7 @@ static void launch_fast_cb(const FwdArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB>), dim3(a.n), dim3(1024), 0,
                        st, a);
   } else {
-    hipLaunchKernelGGL((acs_forward_keys<K, Sh::G, Sh::J, Sh::P, CB>), dim3(a.n), dim3(1024), 0,
-                       st, a);
+    hipLaunchKernelGGL((acs_forward_tourn<K, Sh::G, Sh::J, CB>), dim3(a.n), dim3(1024), 0, st, a);
   }
 }
 

@@ -66,8 +66,8 @@ EXL3_HD inline int32_t bits_per_backpointer(int K) {
 // threads and 64 candidate branches per thread per step; P lanes split the
 // 2^K branches of one edge set, Q = 2^K / P per lane):
 //   K : G  J  P   Q   scratch
-//   1 : 16 2  1   2   backpointers (key kernel)
-//   2 :  4 4  1   4   backpointers (key kernel)
+//   1 : 16 2  1   2   backpointers (tournament kernel)
+//   2 :  4 4  1   4   backpointers (tournament kernel)
 //   3 :  4 2  1   8   cost rows (row kernel)
 //   4 :  4 1  1  16   cost rows
 //   5 :  2 1  1  32   cost rows
@@ -101,6 +101,13 @@ EXL3_HD inline BpLayout make_layout(int K) {
 }
 
 // Slot of edge e inside a backpointer row (edge order in cost-row mode).
+// Thread `unit` of the tournament kernel owns one 32-bit word per row. Its
+// packed register pair pp = (g >> 1) * J + j % J holds the edges of groups
+// h0 + 2(g >> 1) (low half, hf = 0) and h0 + 2(g >> 1) + 1 (high half,
+// hf = 1). The kernel gathers pairs 2c and 2c + 1 into the four bytes of
+// one word (byte 2u + hf for pair 2c + u) and stacks the c-th word at bit
+// K * c of every byte, so the field of an edge starts at bit
+// 8 (2u + hf) + K c of the word.
 EXL3_HD inline uint32_t bp_slot(const BpLayout& l, uint32_t e) {
   if (l.natural || l.mode == MODE_COST_ROWS) return e;
   const uint32_t h = e >> l.K;
@@ -109,8 +116,9 @@ EXL3_HD inline uint32_t bp_slot(const BpLayout& l, uint32_t e) {
   const uint32_t NJ = (1u << l.K) / J;
   const uint32_t unit = (h / G) * NJ + j / J;
   const uint32_t g = h % G;
-  const uint32_t local = ((g >> 1) * J + (j % J)) * 2u + (g & 1u);
-  return unit * (G * J) + local;
+  const uint32_t pp = (g >> 1) * J + (j % J);
+  const uint32_t bit = 8u * (2u * (pp & 1u) + (g & 1u)) + (uint32_t)l.K * (pp >> 1);
+  return unit * (G * J) + bit / (uint32_t)l.K;
 }
 
 EXL3_HD inline uint64_t tile_scratch_bytes(const BpLayout& l, int L) {
