@@ -366,30 +366,58 @@ __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
   forward_epilogue<C::NT>(a, C::E, s_cost[L & 1], s_red);
 }
 
-// Tournament forward pass (K = 1, 2): first minimum over the 2^K branches by
-// a packed knockout. For a register pair E_q = [cost of edge b | edge a] at
-// branch q, a match of q0 < q1 keeps min(E_q0, E_q1) (v_pk_min_u16) and
-// records q1 as the winner only when E_q1 < E_q0 strictly: the sign bit of
-// v_pk_sub_i16 (exact since costs lie in [0, 0x7C00]). The lower branch wins
-// ties, so the final winner is the reference's first minimum.
-// The winners' bits sit at bits 15 and 31 of each difference word; v_perm
-// gathers the bytes holding them for two register pairs into one word (bit
-// 7 of each byte), and a byte-wise shift register (shift right by one,
-// insert at bit 7) stacks eight such words into the thread's 32-bit
-// backpointer word, in bp_slot order.
+// Tournament forward pass (K = 1, 2). Thread `unit` owns every edge of
+// groups h0 .. h0 + G - 1 (h0 = unit * G); a packed register pair holds
+// edges j and j + 1 (j even) of one group. Both halves share the group's
+// 2^K predecessor costs, so the FMA takes its addend broadcast from one half
+// of a 32-bit LDS word holding two groups' costs (op_sel, no extra work),
+// and the pair's minima are already in edge order for 32-bit LDS stores.
+// First minimum over branches by a packed knockout: for E_q = [cost of
+// edge j+1 | edge j] at branch q, a match of q0 < q1 keeps
+// min(E_q0, E_q1) (v_pk_min_u16) and records q1 as the winner only when
+// E_q1 < E_q0 strictly: the sign bit of v_pk_sub_i16 (exact since costs lie
+// in [0, 0x7C00]). The lower branch wins ties, so the final winner is the
+// reference's first minimum. The winners' bits sit at bits 15 and 31 of each
+// difference word. v_perm's sign-replicating selectors (8..11: bit 15 or 31
+// of a source copied to all eight bits of a byte) turn two register pairs
+// into four 0x00/0xFF bytes, and one v_bitop3 puts them at bit s of every
+// byte of the thread's 32-bit backpointer word (s = insertion order,
+// bp_slot layout).
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t bfi32(uint32_t mask, uint32_t a, uint32_t b) {
   return (mask & a) | (~mask & b);
 }
 
-// Bytes 1 and 3 of `lo_pair` (its sign bits), then bytes 1 and 3 of `hi_pair`.
-__device__ __forceinline__ uint32_t gather_signs(uint32_t lo_pair, uint32_t hi_pair) {
-  return __builtin_amdgcn_perm(lo_pair, hi_pair, 0x03010705u);
+// Byte 0: bit 15 of `lo_pair`, byte 1: its bit 31, bytes 2, 3: bits 15, 31
+// of `hi_pair`, each replicated to 0x00 / 0xFF (v_perm selectors 10, 11, 8,
+// 9; `lo_pair` is the first source).
+__device__ __forceinline__ uint32_t sign_bytes(uint32_t lo_pair, uint32_t hi_pair) {
+  return __builtin_amdgcn_perm(lo_pair, hi_pair, 0x09080B0Au);
 }
 
-__device__ __forceinline__ uint32_t push_signs(uint32_t acc, uint32_t signs) {
-  return bfi32(0x80808080u, signs, acc >> 1);
+// acc with bit s of every byte taken from `signs`: v_bitop3 with truth table
+// 0xCA is (mask ? signs : acc), one instruction per insert.
+__device__ __forceinline__ uint32_t insert_signs(uint32_t acc, uint32_t signs, int s) {
+  return __builtin_amdgcn_bitop3_b32(0x01010101u << s, signs, acc, 0xCA);
+}
+
+template <int K, int G, int CB>
+__device__ __forceinline__ void load_codebook_jpairs(f16x2 (&cbv)[G][(1 << K) / 2][1 << K],
+                                                     int h0) {
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int jp = 0; jp < (1 << K) / 2; ++jp)
+#pragma unroll
+      for (int q = 0; q < (1 << K); ++q) {
+        const uint32_t s_lo =
+            ((uint32_t)q << (16 - K)) | ((uint32_t)(h0 + g) << K) | (uint32_t)(2 * jp);
+        f16x2 v;
+        v.x = decode_state(CB, s_lo);
+        v.y = decode_state(CB, s_lo + 1u);
+        cbv[g][jp][q] = v;
+      }
 }
 
 template <int K, int G, int J, int CB>
@@ -397,22 +425,21 @@ __global__ void __launch_bounds__(1024) acs_forward_tourn(FwdArgs a) {
   constexpr int P = 1;
   using C = FastCfg<K, G, J, P>;
   static_assert(K == 1 || K == 2, "tournament kernel handles 2 or 4 branches");
+  static_assert(J == (1 << K), "a thread owns whole groups");
   static_assert(G * J * K == 32, "one 32-bit backpointer word per thread and step");
-  constexpr int PAIRS = (G / 2) * J;
+  constexpr int JP = J / 2;
+  constexpr int PAIRS = G * JP;
   static_assert(PAIRS * K == 16, "eight sign words per backpointer word");
   __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][C::E];
   __shared__ f16 s_w[256];
   __shared__ uint32_t s_red[16];
 
   const int L = a.L;
-  const int tid = threadIdx.x;
-  const int unit = tid;
-  const int jj = unit % C::NJ;
-  const int gq = unit / C::NJ;
-  const int h0 = gq * G;
+  const int unit = threadIdx.x;
+  const int h0 = unit * G;
 
-  f16x2 cbv[G / 2][J][C::Q];
-  load_codebook<K, G, J, C::Q, C::KR, CB>(cbv, 0, jj, h0);
+  f16x2 cbv[G][JP][C::Q];
+  load_codebook_jpairs<K, G, CB>(cbv, h0);
   int pre;
   forward_prologue<C::NT>(a, C::E, false, s_w, s_cost[0], pre);
   __syncthreads();
@@ -422,34 +449,38 @@ __global__ void __launch_bounds__(1024) acs_forward_tourn(FwdArgs a) {
     int ri = i + a.roll;
     if (ri >= L) ri -= L;
     const uint16_t* cin = s_cost[i & 1];
-    uint16_t* cout = s_cost[(i & 1) ^ 1];
+    uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[(i & 1) ^ 1]);
     const f16 w = s_w[ri];
     f16x2 w2;
     w2.x = w;
     w2.y = w;
 
-    uint32_t cpair[C::Q][G / 2];
+    // Predecessor costs of branch q for groups h0 + 2 g2, h0 + 2 g2 + 1.
+    uint32_t cw[C::Q][G / 2];
 #pragma unroll
     for (int q = 0; q < C::Q; ++q) {
       const uint32_t* src = reinterpret_cast<const uint32_t*>(cin + q * C::S + h0);
 #pragma unroll
-      for (int g2 = 0; g2 < G / 2; ++g2) cpair[q][g2] = src[g2];
+      for (int g2 = 0; g2 < G / 2; ++g2) cw[q][g2] = src[g2];
     }
 
     uint32_t acc = 0;
+    uint32_t mout[PAIRS];
 #pragma unroll
     for (int pp0 = 0; pp0 < PAIRS; pp0 += 2) {
       uint32_t lo_bit[2], hi_bit[2];  // sign words: branch bit 0 and (K = 2) bit 1
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int g2 = (pp0 + u) / J;
-        const int jl = (pp0 + u) % J;
+        const int g = (pp0 + u) / JP;
+        const int jp = (pp0 + u) % JP;
         u16x2 e[C::Q];
 #pragma unroll
         for (int q = 0; q < C::Q; ++q) {
-          const f16x2 dh = cbv[g2][jl][q] - w2;
-          e[q] = __builtin_bit_cast(
-              u16x2, __builtin_elementwise_fma(dh, dh, __builtin_bit_cast(f16x2, cpair[q][g2])));
+          const f16x2 cv = __builtin_bit_cast(f16x2, cw[q][g >> 1]);
+          const f16x2 c = (g & 1) ? __builtin_shufflevector(cv, cv, 1, 1)
+                                  : __builtin_shufflevector(cv, cv, 0, 0);
+          const f16x2 dh = cbv[g][jp][q] - w2;
+          e[q] = __builtin_bit_cast(u16x2, __builtin_elementwise_fma(dh, dh, c));
         }
         u16x2 m;
         if constexpr (K == 1) {
@@ -470,13 +501,18 @@ __global__ void __launch_bounds__(1024) acs_forward_tourn(FwdArgs a) {
           hi_bit[u] = dr;
           lo_bit[u] = bfi32(dr, d23, d01);  // the winning side's first match
         }
-        const int ea = ((h0 + 2 * g2) << K) | (jj * J + jl);
-        cout[ea] = m.x;
-        cout[ea + (1 << K)] = m.y;
+        mout[pp0 + u] = __builtin_bit_cast(uint32_t, m);
       }
-      acc = push_signs(acc, gather_signs(lo_bit[0], lo_bit[1]));
-      if constexpr (K == 2) acc = push_signs(acc, gather_signs(hi_bit[0], hi_bit[1]));
+      if constexpr (K == 1) {
+        acc = insert_signs(acc, sign_bytes(lo_bit[0], lo_bit[1]), pp0 / 2);
+      } else {
+        acc = insert_signs(acc, sign_bytes(lo_bit[0], lo_bit[1]), pp0);
+        acc = insert_signs(acc, sign_bytes(hi_bit[0], hi_bit[1]), pp0 + 1);
+      }
     }
+    // Pair pp covers edges 2 pp, 2 pp + 1 of this thread's span.
+#pragma unroll
+    for (int pp = 0; pp < PAIRS; ++pp) cout[unit * PAIRS + pp] = mout[pp];
     if (ri < a.store_rows) reinterpret_cast<uint32_t*>(tile_bp + (int64_t)ri * C::ROWB)[unit] = acc;
     __syncthreads();
   }

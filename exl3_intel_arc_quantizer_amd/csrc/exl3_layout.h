@@ -101,13 +101,13 @@ EXL3_HD inline BpLayout make_layout(int K) {
 }
 
 // Slot of edge e inside a backpointer row (edge order in cost-row mode).
-// Thread `unit` of the tournament kernel owns one 32-bit word per row. Its
-// packed register pair pp = (g >> 1) * J + j % J holds the edges of groups
-// h0 + 2(g >> 1) (low half, hf = 0) and h0 + 2(g >> 1) + 1 (high half,
-// hf = 1). The kernel gathers pairs 2c and 2c + 1 into the four bytes of
-// one word (byte 2u + hf for pair 2c + u) and stacks the c-th word at bit
-// K * c of every byte, so the field of an edge starts at bit
-// 8 (2u + hf) + K c of the word.
+// Thread `unit` of the tournament kernel owns all 2^K edges of groups
+// h0 .. h0 + G - 1 and one 32-bit word per row. Its packed register pair
+// pp = g * (J / 2) + (j >> 1) holds edges j (low half, hf = 0) and j + 1
+// (high half, hf = 1) of group h0 + g, j even. The kernel gathers pairs 2c
+// and 2c + 1 into the four bytes of one word (byte 2u + hf for pair 2c + u)
+// and stacks the c-th word at bit K * c of every byte, so the field of an
+// edge starts at bit 8 (2u + hf) + K c of the word.
 EXL3_HD inline uint32_t bp_slot(const BpLayout& l, uint32_t e) {
   if (l.natural || l.mode == MODE_COST_ROWS) return e;
   const uint32_t h = e >> l.K;
@@ -115,9 +115,9 @@ EXL3_HD inline uint32_t bp_slot(const BpLayout& l, uint32_t e) {
   const uint32_t G = (uint32_t)l.G, J = (uint32_t)l.J;
   const uint32_t NJ = (1u << l.K) / J;
   const uint32_t unit = (h / G) * NJ + j / J;
-  const uint32_t g = h % G;
-  const uint32_t pp = (g >> 1) * J + (j % J);
-  const uint32_t bit = 8u * (2u * (pp & 1u) + (g & 1u)) + (uint32_t)l.K * (pp >> 1);
+  const uint32_t jl = j % J;
+  const uint32_t pp = (h % G) * (J / 2u) + (jl >> 1);
+  const uint32_t bit = 8u * (2u * (pp & 1u) + (jl & 1u)) + (uint32_t)l.K * (pp >> 1);
   return unit * (G * J) + bit / (uint32_t)l.K;
 }
 
