@@ -228,8 +228,8 @@ __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int E, const ui
 // thread and step.
 template <int K>
 struct FastShape {
-  static constexpr int G = (K == 1) ? 16 : (K <= 4 ? 4 : 2);
-  static constexpr int J = (K == 1) ? 2 : (K == 2 ? 4 : (K == 3 ? 2 : 1));
+  static constexpr int G = (K == 1) ? 16 : (K == 2 ? 4 : 1);
+  static constexpr int J = (K == 1) ? 2 : (K == 2 ? 4 : (K == 3 ? 8 : (K == 4 ? 4 : 2)));
   static constexpr int P = (K == 6) ? 2 : (K == 7 ? 4 : 1);
 };
 
@@ -247,7 +247,7 @@ struct FastCfg {
   static constexpr int UNIT_BITS = G * J * BPB;
   static constexpr int ROWB = E * BPB / 8;
   static_assert(NT == 1024, "fast configurations use 1024 threads");
-  static_assert(G % 2 == 0, "groups are processed in packed pairs");
+  static_assert(J % 2 == 0, "edges are processed in packed pairs (j, j + 1)");
   static_assert(P == 1 || P == 2 || P == 4, "branch split within a quad");
 };
 
@@ -275,33 +275,22 @@ __device__ __forceinline__ u16x2 quad_min_u16x2(u16x2 v) {
   return v;
 }
 
-// Codebook values of this thread's candidates: pair (g2, jl, q) holds the
-// states of groups h0+2*g2 (low half) and h0+2*g2+1 (high half), edge
-// j = jj*J + jl, branch k = p*Q + q.
-template <int K, int G, int J, int Q, int KR, int CB>
-__device__ __forceinline__ void load_codebook(f16x2 (&cbv)[G / 2][J][Q], int p, int jj, int h0) {
-#pragma unroll
-  for (int g2 = 0; g2 < G / 2; ++g2)
-#pragma unroll
-    for (int jl = 0; jl < J; ++jl)
-#pragma unroll
-      for (int q = 0; q < Q; ++q) {
-        const uint32_t k = (uint32_t)(p * Q + q);
-        const uint32_t j = (uint32_t)(jj * J + jl);
-        const uint32_t s_lo = (k << KR) | ((uint32_t)(h0 + 2 * g2) << K) | j;
-        f16x2 v;
-        v.x = decode_state(CB, s_lo);
-        v.y = decode_state(CB, s_lo + (1u << K));
-        cbv[g2][jl][q] = v;
-      }
-}
-
 // Cost-row forward pass (K = 3..7): minimum cost per edge, rows to HBM.
-// CB is the codebook selector (compile time keeps the prologue's registers
-// low enough for two workgroups per CU).
-template <int K, int G, int J, int P, int CB>
+// Thread `unit` owns the J edges jj*J .. jj*J + J - 1 of one group h, in
+// packed pairs (j, j + 1), and the Q = 2^K / P branches of lane p of its
+// P-lane quad. All edges of a group share the 2^K predecessor costs, so
+// each cost is one 16-bit LDS read broadcast to both halves of the FMA
+// addend (op_sel), and v_pk_minimum3_f16 folds two candidates per
+// instruction into the running minimum (costs are non-negative fp16 with no
+// NaN, where IEEE minimum returns the same bits as an integer minimum).
+// The pair minima are in edge order for 32-bit LDS stores. CB is the
+// codebook selector (compile time keeps the prologue's registers low enough
+// for two workgroups per CU).
+template <int K, int J, int P, int CB>
 __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
-  using C = FastCfg<K, G, J, P>;
+  using C = FastCfg<K, 1, J, P>;
+  constexpr int JP = J / 2;
+  static_assert(C::Q % 2 == 0, "branches are folded two at a time");
   __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][C::E];
   __shared__ f16 s_w[256];
   __shared__ uint32_t s_red[16];
@@ -311,11 +300,20 @@ __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
   const int p = tid % P;
   const int unit = tid / P;
   const int jj = unit % C::NJ;
-  const int gq = unit / C::NJ;
-  const int h0 = gq * G;
+  const int h = unit / C::NJ;
+  const int ebase = (h << K) | (jj * J);
 
-  f16x2 cbv[G / 2][J][C::Q];
-  load_codebook<K, G, J, C::Q, C::KR, CB>(cbv, p, jj, h0);
+  f16x2 cbv[JP][C::Q];
+#pragma unroll
+  for (int jp = 0; jp < JP; ++jp)
+#pragma unroll
+    for (int q = 0; q < C::Q; ++q) {
+      const uint32_t s_lo = ((uint32_t)(p * C::Q + q) << C::KR) | (uint32_t)(ebase + 2 * jp);
+      f16x2 v;
+      v.x = decode_state(CB, s_lo);
+      v.y = decode_state(CB, s_lo + 1u);
+      cbv[jp][q] = v;
+    }
   int pre;
   forward_prologue<C::NT>(a, C::E, true, s_w, s_cost[0], pre);
   __syncthreads();
@@ -324,43 +322,39 @@ __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
     int ri = i + a.roll;
     if (ri >= L) ri -= L;
     const uint16_t* cin = s_cost[i & 1];
-    uint16_t* cout = s_cost[(i & 1) ^ 1];
+    uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[(i & 1) ^ 1]);
     if (i >= 1 && i - 1 >= a.store_from) store_cost_row<C::NT>(a, C::E, cin, i - 1);
     const f16 w = s_w[ri];
     f16x2 w2;
     w2.x = w;
     w2.y = w;
 
-    u16x2 m[G / 2][J];
+    f16x2 m[JP];
 #pragma unroll
-    for (int q = 0; q < C::Q; ++q) {
-      const uint32_t k = (uint32_t)(p * C::Q + q);
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(cin + k * C::S + h0);
-      uint32_t cpair[G / 2];
+    for (int q = 0; q < C::Q; q += 2) {
+      const int k = p * C::Q + q;
+      const f16 c0 = f16_bits(cin[k * C::S + h]);
+      const f16 c1 = f16_bits(cin[(k + 1) * C::S + h]);
+      f16x2 c0v, c1v;
+      c0v.x = c0;
+      c0v.y = c0;
+      c1v.x = c1;
+      c1v.y = c1;
 #pragma unroll
-      for (int g2 = 0; g2 < G / 2; ++g2) cpair[g2] = src[g2];
-#pragma unroll
-      for (int g2 = 0; g2 < G / 2; ++g2)
-#pragma unroll
-        for (int jl = 0; jl < J; ++jl) {
-          const f16x2 dh = cbv[g2][jl][q] - w2;
-          const f16x2 err =
-              __builtin_elementwise_fma(dh, dh, __builtin_bit_cast(f16x2, cpair[g2]));
-          const u16x2 eu = __builtin_bit_cast(u16x2, err);
-          m[g2][jl] = (q == 0) ? eu : __builtin_elementwise_min(m[g2][jl], eu);
-        }
+      for (int jp = 0; jp < JP; ++jp) {
+        const f16x2 d0 = cbv[jp][q] - w2;
+        const f16x2 d1 = cbv[jp][q + 1] - w2;
+        const f16x2 e0 = __builtin_elementwise_fma(d0, d0, c0v);
+        const f16x2 e1 = __builtin_elementwise_fma(d1, d1, c1v);
+        m[jp] = (q == 0) ? __builtin_elementwise_minimum(e0, e1)
+                         : __builtin_elementwise_minimum(__builtin_elementwise_minimum(m[jp], e0), e1);
+      }
     }
 #pragma unroll
-    for (int g2 = 0; g2 < G / 2; ++g2)
-#pragma unroll
-      for (int jl = 0; jl < J; ++jl) {
-        const u16x2 v = quad_min_u16x2<P>(m[g2][jl]);
-        const int e = ((h0 + 2 * g2) << K) | (jj * J + jl);
-        if (P == 1 || p == 0) {
-          cout[e] = v.x;
-          cout[e + (1 << K)] = v.y;
-        }
-      }
+    for (int jp = 0; jp < JP; ++jp) {
+      const u16x2 v = quad_min_u16x2<P>(__builtin_bit_cast(u16x2, m[jp]));
+      if (P == 1 || p == 0) cout[(ebase >> 1) + jp] = __builtin_bit_cast(uint32_t, v);
+    }
     __syncthreads();
   }
   forward_epilogue<C::NT>(a, C::E, s_cost[L & 1], s_red);
@@ -842,7 +836,7 @@ template <int K, int CB>
 static void launch_fast_cb(const FwdArgs& a, hipStream_t st) {
   using Sh = FastShape<K>;
   if constexpr (K >= 3) {
-    hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB>), dim3(a.n), dim3(1024), 0,
+    hipLaunchKernelGGL((acs_forward_rows<K, Sh::J, Sh::P, CB>), dim3(a.n), dim3(1024), 0,
                        st, a);
   } else {
     hipLaunchKernelGGL((acs_forward_tourn<K, Sh::G, Sh::J, CB>), dim3(a.n), dim3(1024), 0, st, a);

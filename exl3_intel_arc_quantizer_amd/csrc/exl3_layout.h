@@ -63,20 +63,23 @@ EXL3_HD inline int32_t bits_per_backpointer(int K) {
 }
 
 // Thread decomposition of the fast forward kernels for each K (all use 1024
-// threads and 64 candidate branches per thread per step; P lanes split the
-// 2^K branches of one edge set, Q = 2^K / P per lane):
+// threads and 64 candidate branches per thread per step). A thread owns J
+// edges of each of G groups, processed in packed pairs (j, j + 1); P lanes
+// split the 2^K branches of one edge set, Q = 2^K / P per lane:
 //   K : G  J  P   Q   scratch
 //   1 : 16 2  1   2   backpointers (tournament kernel)
 //   2 :  4 4  1   4   backpointers (tournament kernel)
-//   3 :  4 2  1   8   cost rows (row kernel)
-//   4 :  4 1  1  16   cost rows
-//   5 :  2 1  1  32   cost rows
-//   6 :  2 1  2  32   cost rows
-//   7 :  2 1  4  32   cost rows
+//   3 :  1 8  1   8   cost rows (row kernel)
+//   4 :  1 4  1  16   cost rows
+//   5 :  1 2  1  32   cost rows
+//   6 :  1 2  2  32   cost rows
+//   7 :  1 2  4  32   cost rows
 // K = 8 has a single group and runs on the generic kernel. Must match
 // FastShape in exl3_encoder.hip.
-EXL3_HD inline int fast_G(int K) { return K == 1 ? 16 : (K <= 4 ? 4 : 2); }
-EXL3_HD inline int fast_J(int K) { return K == 1 ? 2 : (K == 2 ? 4 : (K == 3 ? 2 : 1)); }
+EXL3_HD inline int fast_G(int K) { return K == 1 ? 16 : (K == 2 ? 4 : 1); }
+EXL3_HD inline int fast_J(int K) {
+  return K == 1 ? 2 : (K == 2 ? 4 : (K == 3 ? 8 : (K == 4 ? 4 : 2)));
+}
 EXL3_HD inline int fast_P(int K) { return K == 6 ? 2 : (K == 7 ? 4 : 1); }
 EXL3_HD inline bool has_fast_kernel(int K) { return K >= 1 && K <= 7; }
 
