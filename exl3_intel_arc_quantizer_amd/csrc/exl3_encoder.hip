@@ -209,15 +209,37 @@ __device__ __forceinline__ void forward_epilogue(const FwdArgs& a, int E, const 
   }
 }
 
-// Copy the cost row of step `step` (held in LDS) to the tile's scratch.
+// Copy the cost row of step `step` (held in LDS in edge order) to the
+// tile's scratch in group-major order (exl3::cost_row_pos): 16-byte chunk c
+// holds branches k0 .. k0 + 7 of group h, with (h << K) | k0 = 8c, gathered
+// from LDS edges (k << (16-2K)) | h. The global stores stay contiguous.
+// The chunks go to the first E / 8 threads: leaving the other waves free
+// measured faster than spreading the gather over every wave.
 template <int NT>
-__device__ __forceinline__ void store_cost_row(const FwdArgs& a, int E, const uint16_t* src,
+__device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const uint16_t* src,
                                                int step) {
-  const int chunks = E / 8;  // 16-byte chunks
+  const int E = 65536 >> K;
+  const int ks = 16 - 2 * K;
+  const int chunks = E / 8;
   uint4* dst = reinterpret_cast<uint4*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
                                         (int64_t)step * E * 2);
-  const uint4* s = reinterpret_cast<const uint4*>(src);
-  for (int c = threadIdx.x; c < chunks; c += NT) dst[c] = s[c];
+  for (int c = threadIdx.x; c < chunks; c += NT) {
+    const int h = (8 * c) >> K;
+    const int k0 = (8 * c) & ((1 << K) - 1);
+    uint32_t v[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t lo = src[((k0 + 2 * m) << ks) | h];
+      const uint32_t hi = src[((k0 + 2 * m + 1) << ks) | h];
+      v[m] = lo | (hi << 16);
+    }
+    dst[c] = make_uint4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+// Whether forward step i stores the row of step i - 1.
+__device__ __forceinline__ bool stores_row(const FwdArgs& a, int K, int i) {
+  return i >= 1 && i - 1 >= a.store_from && exl3::cost_row_stored(K, i - 1);
 }
 
 // ------------------------------------------------------------ fast kernels
@@ -277,8 +299,9 @@ __device__ __forceinline__ u16x2 quad_min_u16x2(u16x2 v) {
 
 // Cost-row forward pass (K = 3..7): minimum cost per edge, rows to HBM.
 // Thread `unit` owns the J edges jj*J .. jj*J + J - 1 of one group h, in
-// packed pairs (j, j + 1), and the Q = 2^K / P branches of lane p of its
-// P-lane quad. All edges of a group share the 2^K predecessor costs, so
+// packed pairs (j, j + 1), and the Q = 2^K / P branches k = q*P + p of lane
+// p of its P-lane quad (interleaved, so the quad's LDS reads fall in
+// different banks). All edges of a group share the 2^K predecessor costs, so
 // each cost is one 16-bit LDS read broadcast to both halves of the FMA
 // addend (op_sel), and v_pk_minimum3_f16 folds two candidates per
 // instruction into the running minimum (costs are non-negative fp16 with no
@@ -308,7 +331,7 @@ __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
   for (int jp = 0; jp < JP; ++jp)
 #pragma unroll
     for (int q = 0; q < C::Q; ++q) {
-      const uint32_t s_lo = ((uint32_t)(p * C::Q + q) << C::KR) | (uint32_t)(ebase + 2 * jp);
+      const uint32_t s_lo = ((uint32_t)(q * P + p) << C::KR) | (uint32_t)(ebase + 2 * jp);
       f16x2 v;
       v.x = decode_state(CB, s_lo);
       v.y = decode_state(CB, s_lo + 1u);
@@ -323,7 +346,7 @@ __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
     if (ri >= L) ri -= L;
     const uint16_t* cin = s_cost[i & 1];
     uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[(i & 1) ^ 1]);
-    if (i >= 1 && i - 1 >= a.store_from) store_cost_row<C::NT>(a, C::E, cin, i - 1);
+    if (stores_row(a, K, i)) store_cost_row<C::NT>(a, K, cin, i - 1);
     const f16 w = s_w[ri];
     f16x2 w2;
     w2.x = w;
@@ -332,9 +355,9 @@ __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
     f16x2 m[JP];
 #pragma unroll
     for (int q = 0; q < C::Q; q += 2) {
-      const int k = p * C::Q + q;
+      const int k = q * P + p;
       const f16 c0 = f16_bits(cin[k * C::S + h]);
-      const f16 c1 = f16_bits(cin[(k + 1) * C::S + h]);
+      const f16 c1 = f16_bits(cin[(k + P) * C::S + h]);
       f16x2 c0v, c1v;
       c0v.x = c0;
       c0v.y = c0;
@@ -549,7 +572,7 @@ __global__ void __launch_bounds__(GEN_NT) acs_forward_generic(FwdArgs a, int K) 
     uint32_t* row = s_row[i & 1];
     uint32_t* done = s_row[(i & 1) ^ 1];
     if (rows) {
-      if (i >= 1 && i - 1 >= a.store_from) store_cost_row<GEN_NT>(a, E, cin, i - 1);
+      if (stores_row(a, K, i)) store_cost_row<GEN_NT>(a, K, cin, i - 1);
     } else if (prev_ri >= 0) {
       // Flush the previous step's backpointer row (complete since the last
       // barrier) and clear it for the step after this one.
@@ -666,12 +689,39 @@ __global__ void __launch_bounds__(256) traceback_kernel(TbArgs a) {
       if (ri >= L) ri -= L;
       const f16 w = f16_bits(wbits[ri]);
       const uint16_t* prow = reinterpret_cast<const uint16_t*>(blk) + (int64_t)(i - 1) * E;
+      // Odd rows of a sparse layout: costs of step i-1 from row i-2.
+      const bool recompute = i >= 1 && !exl3::cost_row_stored(K, i - 1);
+      const f16 w1 = f16_bits(wbits[ri == 0 ? L - 1 : ri - 1]);
+      const uint16_t* prow2 = prow - E;
+      const uint32_t h = edge >> K;
       uint32_t key = 0xFFFFFFFFu;
       for (int k = lane; k < NB; k += GL) {
         const uint32_t sigma = ((uint32_t)k << KR) | edge;
         const uint32_t pred = sigma >> K;
-        const uint16_t cbits =
-            (i == 0) ? ((pre < 0 || (int)pred == pre) ? 0 : 0x7C00) : prow[pred];
+        uint16_t cbits;
+        if (i == 0) {
+          cbits = (pre < 0 || (int)pred == pre) ? 0 : 0x7C00;
+        } else if (!recompute) {
+          cbits = prow[(h << K) | (uint32_t)k];
+        } else {
+          // cost_{i-1}[pred] = min over k2 of fma(dh, dh, cost_{i-2}[p2]),
+          // p2 = (k2 << (16-2K)) | (pred >> K): one chunk of row i-2.
+          const uint4* chunk =
+              reinterpret_cast<const uint4*>(prow2 + ((int64_t)(pred >> K) << K));
+          uint32_t best = 0xFFFFu;
+          for (int c = 0; c < NB / 8; ++c) {
+            const uint4 q = chunk[c];
+            const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+              const uint32_t k2 = (uint32_t)(8 * c + m);
+              const uint32_t c2 = (words[m >> 1] >> (16 * (m & 1))) & 0xFFFFu;
+              const f16 d2 = decode_state(a.cb, (k2 << KR) | pred) - w1;
+              best = min(best, (uint32_t)bits_f16(__builtin_fmaf16(d2, d2, f16_bits(c2))));
+            }
+          }
+          cbits = (uint16_t)best;
+        }
         const f16 dh = decode_state(a.cb, sigma) - w;
         const f16 err = __builtin_fmaf16(dh, dh, f16_bits(cbits));
         key = umin(key, ((uint32_t)bits_f16(err) << 16) | (uint32_t)k);
@@ -1020,7 +1070,7 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
     // 0..L/2-1 only, i.e. forward steps L/2..L-1 (reference_encoder.py:284-288).
     a.roll = L / 2;
     a.store_rows = L / 2;
-    a.store_from = L / 2 - 1;
+    a.store_from = exl3::first_needed_row(K, L);
     a.cost_slot = 0;
     a.best_edges = best_edges;
     a.best_stride = hstride;

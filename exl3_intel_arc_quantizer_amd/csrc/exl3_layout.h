@@ -20,13 +20,19 @@
 //   the fast kernel's thread `unit` owns G*J consecutive slots and writes
 //   them with one 32-bit store per step; bp_slot() maps an edge to its slot.
 //   Row r holds ring row r.
-// * cost rows (K = 3..7): the fp16 path-cost vector after each step
-//   (E * 2 bytes, edge order). The forward pass then only needs the minimum
-//   cost per edge, which packed fp16 arithmetic computes at the VALU roofline,
-//   and the traceback recomputes the 2^K candidates of the one edge on the
-//   path from row i-1 (the costs the forward step i read). Row i holds the
-//   output of trellis step i (step order, independent of the ring roll).
-//   For K <= 2 these rows would outweigh the HBM budget (32-64 KiB/step).
+// * cost rows (K = 3..7): the fp16 path-cost vector after a step (E * 2
+//   bytes). The forward pass then only needs the minimum cost per edge, which
+//   packed fp16 arithmetic computes at the VALU roofline, and the traceback
+//   recomputes the 2^K candidates of the one edge on the path from row i-1
+//   (the costs the forward step i read). Row i holds the output of trellis
+//   step i (step order, independent of the ring roll). A row is group-major:
+//   predecessor edge x = (k << (16-2K)) | h sits at position (h << K) | k,
+//   so the 2^K costs one traceback step reads are one contiguous chunk. At
+//   K = 3..5 only even steps are stored (the rows are 16-64 KiB of HBM
+//   writes per step); for an odd row the traceback recomputes the 2^K
+//   costs it needs, each a minimum over 2^K candidates from the chunk of
+//   row i-2 that the forward pass read. For K <= 2 rows would outweigh the
+//   HBM budget (32-64 KiB/step).
 //
 // Per-tile block: (L + 1) rows of row_bytes. Row L is a header:
 //   int32 [0] pass-1 terminal edge, [1] end state, [2] pre_state of the last
@@ -103,7 +109,23 @@ EXL3_HD inline BpLayout make_layout(int K) {
   return l;
 }
 
-// Slot of edge e inside a backpointer row (edge order in cost-row mode).
+// Cost rows: which steps are stored, and where edge x sits in a row.
+EXL3_HD inline bool sparse_cost_rows(int K) { return K >= 3 && K <= 5; }
+EXL3_HD inline bool cost_row_stored(int K, int step) {
+  return !sparse_cost_rows(K) || (step & 1) == 0;
+}
+EXL3_HD inline uint32_t cost_row_pos(int K, uint32_t x) {
+  const int ks = 16 - 2 * K;
+  return ((x & ((1u << ks) - 1u)) << K) | (x >> ks);
+}
+// First row the pass-1 traceback reaches (it covers steps L-1 .. L/2 and
+// reads rows L/2-1 .. L-2; an odd row needs the even row before it).
+EXL3_HD inline int first_needed_row(int K, int L) {
+  const int r = L / 2 - 1;
+  return sparse_cost_rows(K) ? (r & ~1) : r;
+}
+
+// Slot of edge e inside a scratch row: cost_row_pos in cost-row mode.
 // Thread `unit` of the tournament kernel owns all 2^K edges of groups
 // h0 .. h0 + G - 1 and one 32-bit word per row. Its packed register pair
 // pp = g * (J / 2) + (j >> 1) holds edges j (low half, hf = 0) and j + 1
@@ -112,7 +134,8 @@ EXL3_HD inline BpLayout make_layout(int K) {
 // and stacks the c-th word at bit K * c of every byte, so the field of an
 // edge starts at bit 8 (2u + hf) + K c of the word.
 EXL3_HD inline uint32_t bp_slot(const BpLayout& l, uint32_t e) {
-  if (l.natural || l.mode == MODE_COST_ROWS) return e;
+  if (l.mode == MODE_COST_ROWS) return cost_row_pos(l.K, e);
+  if (l.natural) return e;
   const uint32_t h = e >> l.K;
   const uint32_t j = e & ((1u << l.K) - 1u);
   const uint32_t G = (uint32_t)l.G, J = (uint32_t)l.J;

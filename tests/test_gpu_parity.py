@@ -164,9 +164,10 @@ def test_forward_pass_pins(ext, torch_mod, generic):
     """Split forward pass (quantize_xpu.cpp:169-215) against the reference's
     forward(): terminal costs bit-exact; in backpointer mode (K = 1, 2, 8) the
     full predecessor table against its hash; in cost-row mode (K = 3..7) every
-    stored cost row against the C oracle's per-step costs. Then the split
-    backward pass reaches the reference's end state."""
-    from exl3_intel_arc_quantizer_amd._native import row_bytes
+    stored cost row (even steps only at K = 3..5, group-major positions)
+    against the C oracle's per-step costs. Then the split backward pass, which
+    recomputes the odd rows, reaches the reference's end state."""
+    from exl3_intel_arc_quantizer_amd._native import load_library, row_bytes
     from exl3_intel_arc_quantizer_amd.scratch_estimator import uses_cost_rows
     g = load_golden("forward_pass")
     for i in range(4):
@@ -194,7 +195,13 @@ def test_forward_pass_pins(ext, torch_mod, generic):
             _, _, want_rows = c_oracle.forward_pass(tile16, K=K, cb=2, roll=roll, pre_state=pre,
                                                     with_rows=True)
             got_rows = block[:255].view(np.uint16).reshape(255, E)
-            np.testing.assert_array_equal(got_rows, want_rows[:255])
+            lib = load_library()
+            pos = np.array([lib.exl3_backpointer_slot(K, e) for e in range(E)], dtype=np.int64)
+            sparse = 3 <= K <= 5
+            for r in range(255):
+                if sparse and r % 2:
+                    continue
+                np.testing.assert_array_equal(got_rows[r][pos], want_rows[r], err_msg=f"row {r}")
             hdr = block[256]
             np.testing.assert_array_equal(hdr[16:16 + 512].view(np.uint16), tile16.view(np.uint16))
             assert int(hdr[8:12].view(np.int32)[0]) == pre

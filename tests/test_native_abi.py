@@ -65,6 +65,17 @@ def test_backpointer_slots_are_a_permutation(K):
     assert lib.exl3_backpointer_slot(K, E) == -1
 
 
+@pytest.mark.parametrize("K", range(3, 8))
+def test_cost_row_positions_are_group_major(K):
+    """Cost rows hold predecessor edge x = (k << (16-2K)) | h at (h << K) | k."""
+    lib = _native.load_library()
+    ks = 16 - 2 * K
+    rng = np.random.default_rng(K)
+    for x in rng.integers(0, 65536 >> K, size=64):
+        k, h = int(x) >> ks, int(x) & ((1 << ks) - 1)
+        assert lib.exl3_backpointer_slot(K, int(x)) == (h << K) | k
+
+
 @pytest.mark.parametrize("K,cb,L,msg", [
     (0, 2, 256, "K must be in 1..8"),
     (9, 2, 256, "K must be in 1..8"),
