@@ -19,7 +19,13 @@ HIP events on the stream the kernel runs on. Peak = 256 CU * 64 lanes * 2
 (packed fp16) * 2.4 GHz = 78.64 T fp16 element-ops/s (the published
 157.3 TFLOP/s fp16 vector rate counts each FMA twice).
 
+``traffic``: HBM bytes per forward launch from the committed rocprofv3 PMC
+summary (profiles/forward_pass_pmc_config2.md): FETCH_SIZE x 2 + WRITE_SIZE
+x 1.0 per dispatch, the factors a 1 GiB device copy reads on the same
+counters; null when the summary has no row for the kernel.
+
     python bench.py [--steps 10] [--warmup 2] [--sweep] [--no-cpu-baseline]
+    python bench.py --profile-forward --k-list 4,2   # forward launches only
 """
 
 from __future__ import annotations
@@ -55,7 +61,7 @@ class DeviceBatch:
     """A batch prepared on the device with its scratch, ready to encode."""
 
     def __init__(self, raw_np, K, torch, ext, batch_cap=None):
-        from exl3_intel_arc_quantizer_amd._native import row_bytes
+        from exl3_intel_arc_quantizer_amd._native import edges_shape
         self.torch, self.ext, self.K = torch, ext, K
         self.n = raw_np.shape[0]
         self.raw = torch.from_numpy(raw_np).cuda()
@@ -64,7 +70,7 @@ class DeviceBatch:
         cap = batch_cap or self.n
         self.cap = cap
         self.costs = torch.empty((cap, 2, 65536 >> K), dtype=torch.float16, device="cuda")
-        self.edges = torch.empty((cap, 257, row_bytes(K)), dtype=torch.uint8, device="cuda")
+        self.edges = torch.empty(edges_shape(cap, K), dtype=torch.uint8, device="cuda")
         self.out_w = torch.empty((self.n, 256), dtype=torch.float32, device="cuda")
         self.out_i = torch.empty((self.n, 256), dtype=torch.int16, device="cuda")
         self.packed = torch.empty((self.n, 16 * K), dtype=torch.int16, device="cuda")
@@ -96,11 +102,28 @@ def time_steps(batch, steps, warmup, torch):
     return (time.perf_counter() - t0) / steps
 
 
+PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                           "forward_pass_pmc_config2.md")
+
+
+def pmc_traffic(K, tiles):
+    """HBM bytes per forward launch of `tiles` tiles at bitrate K from the
+    committed PMC summary (rows `| traffic | K | tiles | bytes |`), scaled
+    linearly in the tile count; None if absent."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 4 and cells[0] == "traffic" and cells[1] == str(K):
+                    return int(round(float(cells[3]) * tiles / float(cells[2])))
+    except OSError:
+        return None
+    return None
+
+
 def forward_kernel_name(K):
     """The forward kernel the fast path launches for bitrate K."""
-    if K in (1, 2):
-        return f"acs_forward_tourn<K={K}>"
-    if 3 <= K <= 7:
+    if 1 <= K <= 7:
         return f"acs_forward_rows<K={K}>"
     return "acs_forward_generic"
 
@@ -124,11 +147,13 @@ def forward_kernel_roofline(batch, torch, reps=3):
     achieved = ops / (ms * 1e-3)
     return {"bound": "valu", "achieved": round(achieved / 1e12, 3),
             "peak": round(PEAK_ELEM_OPS / 1e12, 3), "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_ELEM_OPS, 4), "traffic": None,
+            "frac": round(achieved / PEAK_ELEM_OPS, 4), "traffic": pmc_traffic(batch.K, n),
             "kernel": forward_kernel_name(batch.K), "launch_ms": round(ms, 3),
             "tiles_per_launch": n,
             "ops_note": "fp16 element-ops: tiles*256 steps*65536 candidates*3 (sub, FMA, "
-                        "compare-select); peak 256 CU*64 lanes*2 halves*2.4 GHz"}
+                        "compare-select); peak 256 CU*64 lanes*2 halves*2.4 GHz",
+            "traffic_note": "HBM bytes per launch: rocprofv3 FETCH_SIZE*2 + WRITE_SIZE*1.0 "
+                            "(copy-kernel calibration), profiles/forward_pass_pmc_config2.md"}
 
 
 def cpu_baseline(tiles, K):
@@ -156,6 +181,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--k-list", default="4,2",
                     help="bitrates to time on configs[1]; the first is the headline value")
+    ap.add_argument("--profile-forward", action="store_true",
+                    help="only the forward launches the roofline is measured on (one warm-up "
+                         "and three timed per K), for rocprofv3 runs")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device copy (known-size kernel for PMC byte "
                          "counter calibration)")
@@ -182,6 +210,17 @@ def main() -> int:
         torch.cuda.empty_cache()
 
     k_list = [int(k) for k in args.k_list.split(",")]
+    if args.profile_forward:
+        for K in k_list:
+            b = DeviceBatch(tiles, K, torch, ext)
+            for _ in range(8):                   # clocks up, as after the timed steps
+                b.forward_only(b.n)
+            rf = forward_kernel_roofline(b, torch)
+            print(f"# K={K}: forward {rf['launch_ms']} ms over {b.n} tiles = "
+                  f"{100 * rf['frac']:.1f}% of VALU peak", file=sys.stderr, flush=True)
+            del b
+            torch.cuda.empty_cache()
+        return 0
     results = {}
     for K in k_list:
         b = DeviceBatch(tiles, K, torch, ext)

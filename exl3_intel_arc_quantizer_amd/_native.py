@@ -128,7 +128,19 @@ def _stream(device_index: int) -> int:
 
 
 def row_bytes(K: int) -> int:
+    """Bytes of one scratch row at bitrate K."""
     return int(load_library().exl3_scratch_row_bytes(K))
+
+
+def tile_rows(K: int, L: int = 256) -> int:
+    """Scratch rows per tile (stored cost rows or ring rows, plus a header)."""
+    lib = load_library()
+    return int(lib.exl3_scratch_edges_bytes(K, L, 1) // lib.exl3_scratch_row_bytes(K))
+
+
+def edges_shape(B: int, K: int, L: int = 256) -> tuple:
+    """Shape of a uint8 ``temp_edges`` scratch tensor for B tiles."""
+    return (B, tile_rows(K, L), row_bytes(K))
 
 
 class QuantizeExtension:
@@ -161,11 +173,12 @@ class QuantizeExtension:
             raise RuntimeError("temp_costs batch dimension B must be >= 1")
         if temp_costs.size(1) != 2 or temp_costs.size(2) != edges:
             raise RuntimeError("temp_costs must have shape (B, 2, 65536 >> K)")
-        rb = row_bytes(K)
-        if (temp_edges.size(0) < batch_cap or temp_edges.size(1) != L + 1
+        _, rows, rb = edges_shape(batch_cap, K, L)
+        if (temp_edges.size(0) < batch_cap or temp_edges.size(1) != rows
                 or temp_edges.size(2) != rb):
             raise RuntimeError(
-                f"temp_edges must have shape (B, L + 1, {rb}) for K={K} (K-bit backpointer layout)")
+                f"temp_edges must have shape (B, {rows}, {rb}) for K={K}, L={L} "
+                "(cost-row / backpointer scratch layout)")
         return batch_cap
 
     # quantize_xpu.cpp:112-167
@@ -233,7 +246,17 @@ class QuantizeExtension:
             raise RuntimeError("output_indices must be on the same GPU device")
         if _check_device_tensor(end_states, "end_states", torch.int32, 1) != dev:
             raise RuntimeError("end_states must be an int32 GPU tensor")
-        L = temp_edges.size(1) - 1
+        # The tile length is the one (256 or 160) whose scratch row count the
+        # temp_edges tensor has; the two counts differ at every K.
+        _validate_common(K, cb, 256, sg_size)
+        if temp_edges.dim() != 3:
+            raise RuntimeError("temp_edges must be 3-D (B, rows, row_bytes)")
+        matches = [n for n in (256, 160) if tile_rows(K, n) == temp_edges.size(1)]
+        if not matches:
+            raise RuntimeError(f"temp_edges has {temp_edges.size(1)} rows, which fits neither "
+                               f"L=256 ({tile_rows(K, 256)}) nor L=160 ({tile_rows(K, 160)}) "
+                               f"at K={K}")
+        L = matches[0]
         _validate_common(K, cb, L, sg_size)
         batch_cap = self._scratch_checks(temp_costs, temp_edges, K, L, dev)
         if not 0 < num_tiles <= batch_cap:

@@ -5,25 +5,23 @@
 // and its SYCL kernel FusedQuantizeKernel (quantize_kernels.sycl:245-360),
 // re-designed for CDNA4:
 //
-//   acs_forward_rows   K = 3..7. One 1024-thread workgroup per tile, fp16 path
+//   acs_forward_rows   K = 1..7. One 1024-thread workgroup per tile, fp16 path
 //                      costs ping-pong in LDS, each thread owns 64 (edge,
 //                      branch) candidates whose codebook values stay in 32
-//                      VGPRs. A step is three packed-fp16 ops per candidate
-//                      pair (subtract, FMA, unsigned-16 min): the minimum cost
-//                      per edge only. Each step's cost row goes to HBM with
-//                      coalesced 16-byte stores; the traceback recomputes the
+//                      VGPRs. A step is a packed subtract and FMA per
+//                      candidate pair plus v_pk_minimum3_f16 folding two pairs
+//                      per instruction: the minimum cost per edge only. Every
+//                      row_stride(K)-th cost row goes to HBM (group-major,
+//                      coalesced 16-byte stores); the traceback recomputes the
 //                      argmin of the one edge on the path.
-//   acs_forward_tourn  K = 1, 2 (cost rows would cost 32-64 KiB per step):
-//                      the first minimum over branches by a packed knockout
-//                      (v_pk_min_u16 + the sign of v_pk_sub_i16 per match);
-//                      winning branches leave as K-bit backpointers.
 //   acs_forward_generic reference-structured kernel (one edge per thread
 //                      iteration, codebook decoded per candidate, strict fp16
 //                      '<' scan): K = 8 and the force_global_costs variant;
 //                      writes the same scratch layout as the fast kernels.
-//   traceback_kernel   walks the ring backwards (one lane per tile over
-//                      backpointers, or 2^K lanes per tile recomputing the
-//                      candidates from cost rows).
+//   traceback_rows_kernel one 64-lane workgroup per tile walks the ring
+//                      backwards, rebuilding the costs of unstored steps from
+//                      the last stored row; traceback_bp_kernel (K = 8) reads
+//                      one backpointer byte per step.
 //   finalize_kernel    packing, path cost, distortion, un-permutation.
 //
 // Numerics (bit-exact vs the reference on finite / infinite inputs):
@@ -209,45 +207,44 @@ __device__ __forceinline__ void forward_epilogue(const FwdArgs& a, int E, const 
   }
 }
 
-// Copy the cost row of step `step` (held in LDS in edge order) to the
-// tile's scratch in group-major order (exl3::cost_row_pos): 16-byte chunk c
-// holds branches k0 .. k0 + 7 of group h, with (h << K) | k0 = 8c, gathered
-// from LDS edges (k << (16-2K)) | h. The global stores stay contiguous.
-// The chunks go to the first E / 8 threads: leaving the other waves free
-// measured faster than spreading the gather over every wave.
+// Copy the cost row of step `step` (held in LDS in edge order) to its slot
+// in the tile's scratch, group-major (exl3::cost_row_pos): position t holds
+// edge (k << (16-2K)) | h for t = (h << K) | k. 16-byte chunk c covers
+// positions 8c .. 8c + 7, gathered from LDS; the global stores stay
+// contiguous. The chunks go to the first E / 8 threads: leaving the other
+// waves free measured faster than spreading the gather over every wave.
 template <int NT>
 __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const uint16_t* src,
                                                int step) {
+  const BpLayout lay = exl3::make_layout(K);
   const int E = 65536 >> K;
   const int ks = 16 - 2 * K;
   const int chunks = E / 8;
   uint4* dst = reinterpret_cast<uint4*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
-                                        (int64_t)step * E * 2);
+                                        (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
   for (int c = threadIdx.x; c < chunks; c += NT) {
-    const int h = (8 * c) >> K;
-    const int k0 = (8 * c) & ((1 << K) - 1);
     uint32_t v[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      const uint32_t lo = src[((k0 + 2 * m) << ks) | h];
-      const uint32_t hi = src[((k0 + 2 * m + 1) << ks) | h];
+      const int t0 = 8 * c + 2 * m, t1 = t0 + 1;
+      const uint32_t lo = src[((t0 & ((1 << K) - 1)) << ks) | (t0 >> K)];
+      const uint32_t hi = src[((t1 & ((1 << K) - 1)) << ks) | (t1 >> K)];
       v[m] = lo | (hi << 16);
     }
     dst[c] = make_uint4(v[0], v[1], v[2], v[3]);
   }
 }
 
-// Whether forward step i stores the row of step i - 1.
+// Whether forward step i stores the cost row of step i - 1.
 __device__ __forceinline__ bool stores_row(const FwdArgs& a, int K, int i) {
-  return i >= 1 && i - 1 >= a.store_from && exl3::cost_row_stored(K, i - 1);
+  return i >= 1 && i - 1 >= a.store_from && exl3::cost_row_stored(exl3::make_layout(K), i - 1);
 }
 
 // ------------------------------------------------------------ fast kernels
 
-// Thread decomposition per K; exl3_layout.h keeps the same table for the
-// backpointer slots. G groups x J edges x Q branches per lane, P lanes share
-// one edge set and split its 2^K branches; 1024 threads, 64 candidates per
-// thread and step.
+// Thread decomposition per K (exl3_layout.h keeps the same table): G groups x
+// J edges x Q branches per lane, P lanes share one edge set and split its
+// 2^K branches; 1024 threads, 64 candidates per thread and step.
 template <int K>
 struct FastShape {
   static constexpr int G = (K == 1) ? 16 : (K == 2 ? 4 : 1);
@@ -265,20 +262,11 @@ struct FastCfg {
   static constexpr int NGQ = S / G;           // group sets
   static constexpr int NT = NGQ * NJ * P;     // threads per tile
   static constexpr int KR = 16 - K;
-  static constexpr int BPB = (K == 3) ? 4 : (K >= 5 ? 8 : K);
-  static constexpr int UNIT_BITS = G * J * BPB;
-  static constexpr int ROWB = E * BPB / 8;
   static_assert(NT == 1024, "fast configurations use 1024 threads");
   static_assert(J % 2 == 0, "edges are processed in packed pairs (j, j + 1)");
+  static_assert(G == 1 || G % 2 == 0, "groups are read in 32-bit pairs");
   static_assert(P == 1 || P == 2 || P == 4, "branch split within a quad");
 };
-
-template <int P>
-__device__ __forceinline__ uint32_t quad_min(uint32_t v) {
-  if (P >= 2) v = umin(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
-  if (P >= 4) v = umin(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
-  return v;
-}
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
@@ -297,21 +285,21 @@ __device__ __forceinline__ u16x2 quad_min_u16x2(u16x2 v) {
   return v;
 }
 
-// Cost-row forward pass (K = 3..7): minimum cost per edge, rows to HBM.
-// Thread `unit` owns the J edges jj*J .. jj*J + J - 1 of one group h, in
-// packed pairs (j, j + 1), and the Q = 2^K / P branches k = q*P + p of lane
-// p of its P-lane quad (interleaved, so the quad's LDS reads fall in
+// Cost-row forward pass (K = 1..7): minimum cost per edge, rows to HBM.
+// Thread `unit` owns edges jj*J .. jj*J + J - 1 of groups h0 .. h0 + G - 1,
+// in packed pairs (j, j + 1), and the Q = 2^K / P branches k = q*P + p of
+// lane p of its P-lane quad (interleaved, so the quad's LDS reads fall in
 // different banks). All edges of a group share the 2^K predecessor costs, so
-// each cost is one 16-bit LDS read broadcast to both halves of the FMA
-// addend (op_sel), and v_pk_minimum3_f16 folds two candidates per
-// instruction into the running minimum (costs are non-negative fp16 with no
-// NaN, where IEEE minimum returns the same bits as an integer minimum).
-// The pair minima are in edge order for 32-bit LDS stores. CB is the
-// codebook selector (compile time keeps the prologue's registers low enough
-// for two workgroups per CU).
-template <int K, int J, int P, int CB>
+// each cost is broadcast to both halves of the FMA addend (op_sel) from a
+// 16-bit LDS read (G = 1) or one half of a 32-bit read holding two groups'
+// costs (G > 1). v_pk_minimum3_f16 folds two candidates per instruction
+// into the running minimum (costs are non-negative fp16 with no NaN, where
+// IEEE minimum returns the same bits as an integer minimum). The pair minima
+// are in edge order for 32-bit LDS stores. CB is the codebook selector
+// (compile time keeps the prologue's registers low).
+template <int K, int G, int J, int P, int CB>
 __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
-  using C = FastCfg<K, 1, J, P>;
+  using C = FastCfg<K, G, J, P>;
   constexpr int JP = J / 2;
   static_assert(C::Q % 2 == 0, "branches are folded two at a time");
   __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][C::E];
@@ -323,20 +311,22 @@ __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
   const int p = tid % P;
   const int unit = tid / P;
   const int jj = unit % C::NJ;
-  const int h = unit / C::NJ;
-  const int ebase = (h << K) | (jj * J);
+  const int h0 = (unit / C::NJ) * G;
 
-  f16x2 cbv[JP][C::Q];
+  f16x2 cbv[G][JP][C::Q];
 #pragma unroll
-  for (int jp = 0; jp < JP; ++jp)
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int q = 0; q < C::Q; ++q) {
-      const uint32_t s_lo = ((uint32_t)(q * P + p) << C::KR) | (uint32_t)(ebase + 2 * jp);
-      f16x2 v;
-      v.x = decode_state(CB, s_lo);
-      v.y = decode_state(CB, s_lo + 1u);
-      cbv[jp][q] = v;
-    }
+    for (int jp = 0; jp < JP; ++jp)
+#pragma unroll
+      for (int q = 0; q < C::Q; ++q) {
+        const uint32_t s_lo = ((uint32_t)(q * P + p) << C::KR) |
+                              ((uint32_t)(h0 + g) << K) | (uint32_t)(jj * J + 2 * jp);
+        f16x2 v;
+        v.x = decode_state(CB, s_lo);
+        v.y = decode_state(CB, s_lo + 1u);
+        cbv[g][jp][q] = v;
+      }
   int pre;
   forward_prologue<C::NT>(a, C::E, true, s_w, s_cost[0], pre);
   __syncthreads();
@@ -352,185 +342,52 @@ __global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
     w2.x = w;
     w2.y = w;
 
-    f16x2 m[JP];
+    f16x2 m[G][JP];
 #pragma unroll
     for (int q = 0; q < C::Q; q += 2) {
       const int k = q * P + p;
-      const f16 c0 = f16_bits(cin[k * C::S + h]);
-      const f16 c1 = f16_bits(cin[(k + P) * C::S + h]);
-      f16x2 c0v, c1v;
-      c0v.x = c0;
-      c0v.y = c0;
-      c1v.x = c1;
-      c1v.y = c1;
+      // cw[b][g2]: predecessor costs of branch k (b = 0) and k + P (b = 1)
+      // for groups h0 + 2 g2 (low half) and h0 + 2 g2 + 1 (high half).
+      uint32_t cw[2][(G + 1) / 2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const uint16_t* src = cin + (k + b * P) * C::S + h0;
+        if constexpr (G == 1) {
+          cw[b][0] = src[0];
+        } else {
+#pragma unroll
+          for (int g2 = 0; g2 < G / 2; ++g2) cw[b][g2] = reinterpret_cast<const uint32_t*>(src)[g2];
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        f16x2 cv[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const f16x2 pair = __builtin_bit_cast(f16x2, cw[b][g >> 1]);
+          cv[b] = (g & 1) ? __builtin_shufflevector(pair, pair, 1, 1)
+                          : __builtin_shufflevector(pair, pair, 0, 0);
+        }
+#pragma unroll
+        for (int jp = 0; jp < JP; ++jp) {
+          const f16x2 d0 = cbv[g][jp][q] - w2;
+          const f16x2 d1 = cbv[g][jp][q + 1] - w2;
+          const f16x2 e0 = __builtin_elementwise_fma(d0, d0, cv[0]);
+          const f16x2 e1 = __builtin_elementwise_fma(d1, d1, cv[1]);
+          m[g][jp] = (q == 0) ? __builtin_elementwise_minimum(e0, e1)
+                              : __builtin_elementwise_minimum(
+                                    __builtin_elementwise_minimum(m[g][jp], e0), e1);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int jp = 0; jp < JP; ++jp) {
-        const f16x2 d0 = cbv[jp][q] - w2;
-        const f16x2 d1 = cbv[jp][q + 1] - w2;
-        const f16x2 e0 = __builtin_elementwise_fma(d0, d0, c0v);
-        const f16x2 e1 = __builtin_elementwise_fma(d1, d1, c1v);
-        m[jp] = (q == 0) ? __builtin_elementwise_minimum(e0, e1)
-                         : __builtin_elementwise_minimum(__builtin_elementwise_minimum(m[jp], e0), e1);
+        const u16x2 v = quad_min_u16x2<P>(__builtin_bit_cast(u16x2, m[g][jp]));
+        const int e = ((h0 + g) << K) | (jj * J + 2 * jp);
+        if (P == 1 || p == 0) cout[e >> 1] = __builtin_bit_cast(uint32_t, v);
       }
-    }
-#pragma unroll
-    for (int jp = 0; jp < JP; ++jp) {
-      const u16x2 v = quad_min_u16x2<P>(__builtin_bit_cast(u16x2, m[jp]));
-      if (P == 1 || p == 0) cout[(ebase >> 1) + jp] = __builtin_bit_cast(uint32_t, v);
-    }
-    __syncthreads();
-  }
-  forward_epilogue<C::NT>(a, C::E, s_cost[L & 1], s_red);
-}
-
-// Tournament forward pass (K = 1, 2). Thread `unit` owns every edge of
-// groups h0 .. h0 + G - 1 (h0 = unit * G); a packed register pair holds
-// edges j and j + 1 (j even) of one group. Both halves share the group's
-// 2^K predecessor costs, so the FMA takes its addend broadcast from one half
-// of a 32-bit LDS word holding two groups' costs (op_sel, no extra work),
-// and the pair's minima are already in edge order for 32-bit LDS stores.
-// First minimum over branches by a packed knockout: for E_q = [cost of
-// edge j+1 | edge j] at branch q, a match of q0 < q1 keeps
-// min(E_q0, E_q1) (v_pk_min_u16) and records q1 as the winner only when
-// E_q1 < E_q0 strictly: the sign bit of v_pk_sub_i16 (exact since costs lie
-// in [0, 0x7C00]). The lower branch wins ties, so the final winner is the
-// reference's first minimum. The winners' bits sit at bits 15 and 31 of each
-// difference word. v_perm's sign-replicating selectors (8..11: bit 15 or 31
-// of a source copied to all eight bits of a byte) turn two register pairs
-// into four 0x00/0xFF bytes, and one v_bitop3 puts them at bit s of every
-// byte of the thread's 32-bit backpointer word (s = insertion order,
-// bp_slot layout).
-typedef short s16x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t bfi32(uint32_t mask, uint32_t a, uint32_t b) {
-  return (mask & a) | (~mask & b);
-}
-
-// Byte 0: bit 15 of `lo_pair`, byte 1: its bit 31, bytes 2, 3: bits 15, 31
-// of `hi_pair`, each replicated to 0x00 / 0xFF (v_perm selectors 10, 11, 8,
-// 9; `lo_pair` is the first source).
-__device__ __forceinline__ uint32_t sign_bytes(uint32_t lo_pair, uint32_t hi_pair) {
-  return __builtin_amdgcn_perm(lo_pair, hi_pair, 0x09080B0Au);
-}
-
-// acc with bit s of every byte taken from `signs`: v_bitop3 with truth table
-// 0xCA is (mask ? signs : acc), one instruction per insert.
-__device__ __forceinline__ uint32_t insert_signs(uint32_t acc, uint32_t signs, int s) {
-  return __builtin_amdgcn_bitop3_b32(0x01010101u << s, signs, acc, 0xCA);
-}
-
-template <int K, int G, int CB>
-__device__ __forceinline__ void load_codebook_jpairs(f16x2 (&cbv)[G][(1 << K) / 2][1 << K],
-                                                     int h0) {
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int jp = 0; jp < (1 << K) / 2; ++jp)
-#pragma unroll
-      for (int q = 0; q < (1 << K); ++q) {
-        const uint32_t s_lo =
-            ((uint32_t)q << (16 - K)) | ((uint32_t)(h0 + g) << K) | (uint32_t)(2 * jp);
-        f16x2 v;
-        v.x = decode_state(CB, s_lo);
-        v.y = decode_state(CB, s_lo + 1u);
-        cbv[g][jp][q] = v;
-      }
-}
-
-template <int K, int G, int J, int CB>
-__global__ void __launch_bounds__(1024) acs_forward_tourn(FwdArgs a) {
-  constexpr int P = 1;
-  using C = FastCfg<K, G, J, P>;
-  static_assert(K == 1 || K == 2, "tournament kernel handles 2 or 4 branches");
-  static_assert(J == (1 << K), "a thread owns whole groups");
-  static_assert(G * J * K == 32, "one 32-bit backpointer word per thread and step");
-  constexpr int JP = J / 2;
-  constexpr int PAIRS = G * JP;
-  static_assert(PAIRS * K == 16, "eight sign words per backpointer word");
-  __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][C::E];
-  __shared__ f16 s_w[256];
-  __shared__ uint32_t s_red[16];
-
-  const int L = a.L;
-  const int unit = threadIdx.x;
-  const int h0 = unit * G;
-
-  f16x2 cbv[G][JP][C::Q];
-  load_codebook_jpairs<K, G, CB>(cbv, h0);
-  int pre;
-  forward_prologue<C::NT>(a, C::E, false, s_w, s_cost[0], pre);
-  __syncthreads();
-  uint8_t* tile_bp = a.scratch + (int64_t)blockIdx.x * a.tile_stride;
-
-  for (int i = 0; i < L; ++i) {
-    int ri = i + a.roll;
-    if (ri >= L) ri -= L;
-    const uint16_t* cin = s_cost[i & 1];
-    uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[(i & 1) ^ 1]);
-    const f16 w = s_w[ri];
-    f16x2 w2;
-    w2.x = w;
-    w2.y = w;
-
-    // Predecessor costs of branch q for groups h0 + 2 g2, h0 + 2 g2 + 1.
-    uint32_t cw[C::Q][G / 2];
-#pragma unroll
-    for (int q = 0; q < C::Q; ++q) {
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(cin + q * C::S + h0);
-#pragma unroll
-      for (int g2 = 0; g2 < G / 2; ++g2) cw[q][g2] = src[g2];
-    }
-
-    uint32_t acc = 0;
-    uint32_t mout[PAIRS];
-#pragma unroll
-    for (int pp0 = 0; pp0 < PAIRS; pp0 += 2) {
-      uint32_t lo_bit[2], hi_bit[2];  // sign words: branch bit 0 and (K = 2) bit 1
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int g = (pp0 + u) / JP;
-        const int jp = (pp0 + u) % JP;
-        u16x2 e[C::Q];
-#pragma unroll
-        for (int q = 0; q < C::Q; ++q) {
-          const f16x2 cv = __builtin_bit_cast(f16x2, cw[q][g >> 1]);
-          const f16x2 c = (g & 1) ? __builtin_shufflevector(cv, cv, 1, 1)
-                                  : __builtin_shufflevector(cv, cv, 0, 0);
-          const f16x2 dh = cbv[g][jp][q] - w2;
-          e[q] = __builtin_bit_cast(u16x2, __builtin_elementwise_fma(dh, dh, c));
-        }
-        u16x2 m;
-        if constexpr (K == 1) {
-          m = __builtin_elementwise_min(e[0], e[1]);
-          lo_bit[u] = __builtin_bit_cast(
-              uint32_t, __builtin_bit_cast(s16x2, e[1]) - __builtin_bit_cast(s16x2, e[0]));
-          hi_bit[u] = 0;
-        } else {
-          const u16x2 m01 = __builtin_elementwise_min(e[0], e[1]);
-          const u16x2 m23 = __builtin_elementwise_min(e[2], e[3]);
-          m = __builtin_elementwise_min(m01, m23);
-          const uint32_t d01 = __builtin_bit_cast(
-              uint32_t, __builtin_bit_cast(s16x2, e[1]) - __builtin_bit_cast(s16x2, e[0]));
-          const uint32_t d23 = __builtin_bit_cast(
-              uint32_t, __builtin_bit_cast(s16x2, e[3]) - __builtin_bit_cast(s16x2, e[2]));
-          const uint32_t dr = __builtin_bit_cast(
-              uint32_t, __builtin_bit_cast(s16x2, m23) - __builtin_bit_cast(s16x2, m01));
-          hi_bit[u] = dr;
-          lo_bit[u] = bfi32(dr, d23, d01);  // the winning side's first match
-        }
-        mout[pp0 + u] = __builtin_bit_cast(uint32_t, m);
-      }
-      if constexpr (K == 1) {
-        acc = insert_signs(acc, sign_bytes(lo_bit[0], lo_bit[1]), pp0 / 2);
-      } else {
-        acc = insert_signs(acc, sign_bytes(lo_bit[0], lo_bit[1]), pp0);
-        acc = insert_signs(acc, sign_bytes(hi_bit[0], hi_bit[1]), pp0 + 1);
-      }
-    }
-    // Pair pp covers edges 2 pp, 2 pp + 1 of this thread's span.
-#pragma unroll
-    for (int pp = 0; pp < PAIRS; ++pp) cout[unit * PAIRS + pp] = mout[pp];
-    if (ri < a.store_rows) reinterpret_cast<uint32_t*>(tile_bp + (int64_t)ri * C::ROWB)[unit] = acc;
     __syncthreads();
   }
   forward_epilogue<C::NT>(a, C::E, s_cost[L & 1], s_red);
@@ -539,13 +396,13 @@ __global__ void __launch_bounds__(1024) acs_forward_tourn(FwdArgs a) {
 // --------------------------------------------------------- generic kernel
 
 constexpr int GEN_NT = 256;
-constexpr int GEN_ROW_WORDS = 1024;  // largest backpointer row: 4 KiB (K = 1, 2)
+constexpr int GEN_ROW_WORDS = 64;  // the K = 8 backpointer row: 256 bytes
 
 // Reference-structured forward pass for any K (reference_encoder.py:130-204,
 // quantize_kernels.sycl:83-157): per edge, scan branches k = 0..2^K-1 with a
 // strict fp16 '<'; codebook decoded per candidate. It writes the scratch
-// layout of K: backpointer rows assembled in LDS (double-buffered, copied out
-// one step later), or cost rows.
+// layout of K: cost rows, or (K = 8) backpointer rows assembled in LDS
+// (double-buffered, copied out one step later).
 __global__ void __launch_bounds__(GEN_NT) acs_forward_generic(FwdArgs a, int K) {
   __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][32768];
   __shared__ uint32_t s_row[2][GEN_ROW_WORDS];
@@ -649,94 +506,193 @@ struct TbArgs {
 // quantize_kernels.sycl:320-333,345-358). write = 0: stop after ring row 0
 // and emit the edge reached (the tail-biting end state). write = 1: emit
 // every state and its codebook value.
-//
-// Backpointer mode: one lane per tile reads k from the row.
-// Cost-row mode: GL = min(2^K, 64) lanes per tile recompute the candidates
-// of the current edge at step i from cost row i-1 (or the initial costs at
-// i = 0) and take the key minimum (lowest branch among equal costs).
-template <int GL>
-__global__ void __launch_bounds__(256) traceback_kernel(TbArgs a) {
-  const int gid = blockIdx.x * blockDim.x + threadIdx.x;
-  const int t = gid / GL;
-  const int lane = gid % GL;
-  if (t >= a.n) return;  // whole lane groups leave together
+
+// Backpointer mode (K = 8): one thread per tile reads k from the row.
+__global__ void __launch_bounds__(256) traceback_bp_kernel(TbArgs a) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= a.n) return;
   const BpLayout& lay = a.lay;
   const int K = lay.K, KR = 16 - K, L = a.L;
   const uint8_t* blk = a.scratch + (int64_t)t * a.tile_stride;
+  uint32_t edge = (uint32_t)a.start[(int64_t)t * a.start_stride] & ((65536u >> K) - 1u);
+  for (int i = L - 1; i >= 0; --i) {
+    int ri = i + a.roll;
+    if (ri >= L) ri -= L;
+    const uint32_t k = read_backpointer(blk + (int64_t)ri * lay.row_bytes, lay, edge);
+    const uint32_t sigma = (k << KR) | edge;
+    if (a.write) {
+      a.out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
+      a.out_w[(int64_t)t * L + ri] = (float)decode_state(a.cb, sigma);
+    }
+    edge = sigma >> K;
+    if (!a.write && ri == 0) break;
+  }
+  if (!a.write) a.end_out[(int64_t)t * a.end_stride] = (int32_t)edge;
+}
+
+// Cost-row mode: one 64-lane wave per tile. At step i with edge e the path's
+// predecessor branch is the key minimum over k of
+// fma(dh, dh, C_{i-1}[(k << (16-2K)) | (e >> K)]) (lowest k among equal
+// costs), dh = fp16(value((k << (16-K)) | e) - w_i). If step i-1 is D > 0
+// steps past the last stored row r0, those 2^K costs are rebuilt from row r0
+// over D levels: level m holds C_{i-1-m} at the positions
+//   x_0 = (k_0 << (16-2K)) | (e >> K),  x_{m+1} = (k_{m+1} << (16-2K)) | (x_m >> K)
+// indexed by the base-2^K digits (k_0 .. k_m); the leaves (level D) are read
+// from row r0, and each level above is, per entry, the minimum over its 2^K
+// children of the forward pass's FMA: exactly the value the forward pass
+// computed for that edge.
+//
+// Leaf n = k_0 .. k_D (k_D least significant) lives in lane n >> RLOG,
+// register n & (R - 1), R = 2^RLOG leaves per lane, so the lowest digits are
+// reduced inside a lane and a lane's leaves are one aligned vector load.
+// Once a level has reduced every register bit, the registers of a lane hold
+// copies of one value and the remaining digits reduce across lanes with
+// __shfl_xor. Trees with fewer than 64 leaves are replicated over the wave.
+
+template <int N>
+struct U16Vec {
+  typedef uint16_t type __attribute__((ext_vector_type(N)));
+};
+
+template <int K>
+__device__ __forceinline__ uint32_t row_pos(uint32_t x) {
+  constexpr int KS = 16 - 2 * K;
+  return ((x & ((1u << KS) - 1u)) << K) | (x >> KS);
+}
+
+template <int K, int CB, int D, bool INIT>
+__device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ row, uint32_t edge,
+                                              const uint16_t* __restrict__ wbits, int ri, int L,
+                                              int lane, int pre) {
+  constexpr int NB = 1 << K, KR = 16 - K, KS = 16 - 2 * K;
+  constexpr int NLOG = K * (D + 1);
+  constexpr int RLOG = NLOG > 6 ? NLOG - 6 : 0;
+  constexpr int R = 1 << RLOG;
+  constexpr uint32_t NMASK = (1u << NLOG) - 1u;
+  constexpr int CH = R < NB ? R : NB;  // leaves per contiguous load
+  const uint32_t h0 = edge >> K;
+
+  uint32_t nid[R];
+  uint32_t xs[R][D + 1];
+  uint32_t v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t n = (((uint32_t)lane << RLOG) | (uint32_t)r) & NMASK;
+    nid[r] = n;
+    uint32_t x = ((n >> (K * D)) << KS) | h0;
+    xs[r][0] = x;
+#pragma unroll
+    for (int m = 1; m <= D; ++m) {
+      x = (((n >> (K * (D - m))) & (NB - 1)) << KS) | (x >> K);
+      xs[r][m] = x;
+    }
+  }
+  if constexpr (INIT) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = (pre < 0 || (int)xs[r][0] == pre) ? 0u : 0x7C00u;
+  } else {
+#pragma unroll
+    for (int c = 0; c < R / CH; ++c) {
+      const typename U16Vec<CH>::type q =
+          *reinterpret_cast<const typename U16Vec<CH>::type*>(row + row_pos<K>(xs[c * CH][D]));
+#pragma unroll
+      for (int u = 0; u < CH; ++u) v[c * CH + u] = q[u];
+    }
+  }
+
+  // Levels D-1 .. 0: reduce digit k_{m+1}, bits [lo, lo + K) of n.
+#pragma unroll
+  for (int m = D - 1; m >= 0; --m) {
+    const int lo = K * (D - 1 - m), hi = lo + K;
+    int rm = ri - 1 - m;
+    if (rm < 0) rm += L;
+    const f16 wm = f16_bits(wbits[rm]);
+    const int nr = lo < RLOG ? R : 1;  // registers still distinct
+#pragma unroll
+    for (int r = 0; r < nr; ++r) {
+      const uint32_t k = (nid[r] >> lo) & (NB - 1);
+      const f16 dh = decode_state(CB, (k << KR) | xs[r][m]) - wm;
+      v[r] = bits_f16(__builtin_fmaf16(dh, dh, f16_bits(v[r])));
+    }
+#pragma unroll
+    for (int b = lo; b < (hi < RLOG ? hi : RLOG); ++b)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (!(r & (1 << b))) {
+          const uint32_t t = umin(v[r], v[r | (1 << b)]);
+          v[r] = t;
+          v[r | (1 << b)] = t;
+        }
+    if (hi > RLOG) {
+#pragma unroll
+      for (int b = (lo > RLOG ? lo : RLOG); b < (hi < NLOG ? hi : NLOG); ++b)
+        v[0] = umin(v[0], (uint32_t)__shfl_xor((int)v[0], 1 << (b - RLOG), 64));
+#pragma unroll
+      for (int r = 1; r < R; ++r) v[r] = v[0];
+    }
+  }
+
+  // Step i: key minimum over k_0, bits [K D, NLOG) of n.
+  const f16 w = f16_bits(wbits[ri]);
+  const int nr = (K * D) < RLOG ? R : 1;
+  uint32_t key = 0xFFFFFFFFu;
+#pragma unroll
+  for (int r = 0; r < nr; ++r) {
+    const uint32_t k0 = nid[r] >> (K * D);
+    const f16 dh = decode_state(CB, (k0 << KR) | edge) - w;
+    const f16 err = __builtin_fmaf16(dh, dh, f16_bits(v[r]));
+    key = umin(key, ((uint32_t)bits_f16(err) << 16) | k0);
+  }
+#pragma unroll
+  for (int b = (K * D > RLOG ? K * D : RLOG); b < NLOG; ++b)
+    key = umin(key, (uint32_t)__shfl_xor((int)key, 1 << (b - RLOG), 64));
+  return key & 0xFFFFu;
+}
+
+// tb_branch for the runtime distance d in [D, row_stride(K)).
+template <int K, int CB, int D>
+__device__ __forceinline__ uint32_t tb_dispatch(int d, const uint16_t* __restrict__ row,
+                                                uint32_t edge, const uint16_t* __restrict__ wbits,
+                                                int ri, int L, int lane, int pre) {
+  if constexpr (D + 1 < exl3::row_stride(K)) {
+    if (d != D) return tb_dispatch<K, CB, D + 1>(d, row, edge, wbits, ri, L, lane, pre);
+  }
+  return tb_branch<K, CB, D, false>(row, edge, wbits, ri, L, lane, pre);
+}
+
+template <int K, int CB>
+__global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
+  constexpr int KR = 16 - K;
+  constexpr int STRIDE = exl3::row_stride(K);
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int L = a.L;
+  const uint8_t* blk = a.scratch + (int64_t)t * a.tile_stride;
   const uint8_t* hdr = blk + a.hdr_offset;
+  const int row_bytes = a.lay.row_bytes;
+  const int pre = reinterpret_cast<const int32_t*>(hdr)[exl3::HDR_PRE_STATE];
+  const uint16_t* wbits = reinterpret_cast<const uint16_t*>(hdr + exl3::HDR_W_BYTES);
   uint32_t edge = (uint32_t)a.start[(int64_t)t * a.start_stride] & ((65536u >> K) - 1u);
 
-  if (lay.mode == exl3::MODE_BACKPOINTERS) {
-    for (int i = L - 1; i >= 0; --i) {
-      int ri = i + a.roll;
-      if (ri >= L) ri -= L;
-      const uint32_t k = read_backpointer(blk + (int64_t)ri * lay.row_bytes, lay, edge);
-      const uint32_t sigma = (k << KR) | edge;
-      if (a.write) {
-        a.out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
-        a.out_w[(int64_t)t * L + ri] = (float)decode_state(a.cb, sigma);
-      }
-      edge = sigma >> K;
-      if (!a.write && ri == 0) break;
+  for (int i = L - 1; i >= 0; --i) {
+    int ri = i + a.roll;
+    if (ri >= L) ri -= L;
+    uint32_t k;
+    if (i == 0) {
+      k = tb_branch<K, CB, 0, true>(nullptr, edge, wbits, ri, L, lane, pre);
+    } else {
+      const int d = (i - 1) % STRIDE;
+      const uint16_t* row = reinterpret_cast<const uint16_t*>(
+          blk + (int64_t)((i - 1 - d) / STRIDE) * row_bytes);
+      k = tb_dispatch<K, CB, 0>(d, row, edge, wbits, ri, L, lane, pre);
     }
-  } else {
-    const int NB = 1 << K;
-    const int pre = reinterpret_cast<const int32_t*>(hdr)[exl3::HDR_PRE_STATE];
-    const uint16_t* wbits = reinterpret_cast<const uint16_t*>(hdr + exl3::HDR_W_BYTES);
-    const int E = 65536 >> K;
-    for (int i = L - 1; i >= 0; --i) {
-      int ri = i + a.roll;
-      if (ri >= L) ri -= L;
-      const f16 w = f16_bits(wbits[ri]);
-      const uint16_t* prow = reinterpret_cast<const uint16_t*>(blk) + (int64_t)(i - 1) * E;
-      // Odd rows of a sparse layout: costs of step i-1 from row i-2.
-      const bool recompute = i >= 1 && !exl3::cost_row_stored(K, i - 1);
-      const f16 w1 = f16_bits(wbits[ri == 0 ? L - 1 : ri - 1]);
-      const uint16_t* prow2 = prow - E;
-      const uint32_t h = edge >> K;
-      uint32_t key = 0xFFFFFFFFu;
-      for (int k = lane; k < NB; k += GL) {
-        const uint32_t sigma = ((uint32_t)k << KR) | edge;
-        const uint32_t pred = sigma >> K;
-        uint16_t cbits;
-        if (i == 0) {
-          cbits = (pre < 0 || (int)pred == pre) ? 0 : 0x7C00;
-        } else if (!recompute) {
-          cbits = prow[(h << K) | (uint32_t)k];
-        } else {
-          // cost_{i-1}[pred] = min over k2 of fma(dh, dh, cost_{i-2}[p2]),
-          // p2 = (k2 << (16-2K)) | (pred >> K): one chunk of row i-2.
-          const uint4* chunk =
-              reinterpret_cast<const uint4*>(prow2 + ((int64_t)(pred >> K) << K));
-          uint32_t best = 0xFFFFu;
-          for (int c = 0; c < NB / 8; ++c) {
-            const uint4 q = chunk[c];
-            const uint32_t words[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-            for (int m = 0; m < 8; ++m) {
-              const uint32_t k2 = (uint32_t)(8 * c + m);
-              const uint32_t c2 = (words[m >> 1] >> (16 * (m & 1))) & 0xFFFFu;
-              const f16 d2 = decode_state(a.cb, (k2 << KR) | pred) - w1;
-              best = min(best, (uint32_t)bits_f16(__builtin_fmaf16(d2, d2, f16_bits(c2))));
-            }
-          }
-          cbits = (uint16_t)best;
-        }
-        const f16 dh = decode_state(a.cb, sigma) - w;
-        const f16 err = __builtin_fmaf16(dh, dh, f16_bits(cbits));
-        key = umin(key, ((uint32_t)bits_f16(err) << 16) | (uint32_t)k);
-      }
-#pragma unroll
-      for (int m = GL / 2; m >= 1; m >>= 1)
-        key = umin(key, (uint32_t)__shfl_xor((int)key, m, GL));
-      const uint32_t sigma = ((key & 0xFFFFu) << KR) | edge;
-      if (a.write && lane == 0) {
-        a.out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
-        a.out_w[(int64_t)t * L + ri] = (float)decode_state(a.cb, sigma);
-      }
-      edge = sigma >> K;
-      if (!a.write && ri == 0) break;
+    const uint32_t sigma = (k << KR) | edge;
+    if (a.write && lane == 0) {
+      a.out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
+      a.out_w[(int64_t)t * L + ri] = (float)decode_state(CB, sigma);
     }
+    edge = sigma >> K;
+    if (!a.write && ri == 0) break;
   }
   if (!a.write && lane == 0) a.end_out[(int64_t)t * a.end_stride] = (int32_t)edge;
 }
@@ -885,12 +841,8 @@ static BpLayout layout_for(int K) { return exl3::make_layout(K); }
 template <int K, int CB>
 static void launch_fast_cb(const FwdArgs& a, hipStream_t st) {
   using Sh = FastShape<K>;
-  if constexpr (K >= 3) {
-    hipLaunchKernelGGL((acs_forward_rows<K, Sh::J, Sh::P, CB>), dim3(a.n), dim3(1024), 0,
-                       st, a);
-  } else {
-    hipLaunchKernelGGL((acs_forward_tourn<K, Sh::G, Sh::J, CB>), dim3(a.n), dim3(1024), 0, st, a);
-  }
+  hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB>), dim3(a.n), dim3(1024), 0, st,
+                     a);
 }
 
 template <int K>
@@ -931,28 +883,37 @@ static FwdArgs forward_args(const float* in, int n, int K, int cb, int L, uint8_
   a.cb = cb;
   a.scratch = scratch;
   a.tile_stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
-  a.hdr_offset = (int64_t)L * lay.row_bytes;
+  a.hdr_offset = exl3::header_offset(lay, L);
   a.term_costs = term_costs;
   a.store_rows = L;
   a.store_from = 0;
   return a;
 }
 
+template <int K>
+static void launch_traceback_rows(const TbArgs& a, hipStream_t st) {
+  switch (a.cb) {
+    case 0: hipLaunchKernelGGL((traceback_rows_kernel<K, 0>), dim3(a.n), dim3(64), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((traceback_rows_kernel<K, 1>), dim3(a.n), dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL((traceback_rows_kernel<K, 2>), dim3(a.n), dim3(64), 0, st, a); break;
+  }
+}
+
 static int launch_traceback(const TbArgs& a, hipStream_t st) {
   if (a.n <= 0) return 0;
-  const int block = 256;
   if (a.lay.mode == exl3::MODE_BACKPOINTERS) {
-    hipLaunchKernelGGL(traceback_kernel<1>, dim3((a.n + block - 1) / block), dim3(block), 0, st,
+    const int block = 256;
+    hipLaunchKernelGGL(traceback_bp_kernel, dim3((a.n + block - 1) / block), dim3(block), 0, st,
                        a);
   } else {
-    const int gl = (1 << a.lay.K) < 64 ? (1 << a.lay.K) : 64;
-    const int64_t threads = (int64_t)a.n * gl;
-    const dim3 grid((unsigned)((threads + block - 1) / block));
-    switch (gl) {
-      case 8: hipLaunchKernelGGL(traceback_kernel<8>, grid, dim3(block), 0, st, a); break;
-      case 16: hipLaunchKernelGGL(traceback_kernel<16>, grid, dim3(block), 0, st, a); break;
-      case 32: hipLaunchKernelGGL(traceback_kernel<32>, grid, dim3(block), 0, st, a); break;
-      default: hipLaunchKernelGGL(traceback_kernel<64>, grid, dim3(block), 0, st, a); break;
+    switch (a.lay.K) {
+      case 1: launch_traceback_rows<1>(a, st); break;
+      case 2: launch_traceback_rows<2>(a, st); break;
+      case 3: launch_traceback_rows<3>(a, st); break;
+      case 4: launch_traceback_rows<4>(a, st); break;
+      case 5: launch_traceback_rows<5>(a, st); break;
+      case 6: launch_traceback_rows<6>(a, st); break;
+      default: launch_traceback_rows<7>(a, st); break;
     }
   }
   return check_launch("traceback");
@@ -964,7 +925,7 @@ static TbArgs traceback_args(const uint8_t* scratch, int n, int K, int cb, int L
   TbArgs t{};
   t.scratch = scratch;
   t.tile_stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
-  t.hdr_offset = (int64_t)L * lay.row_bytes;
+  t.hdr_offset = exl3::header_offset(lay, L);
   t.lay = lay;
   t.n = n;
   t.L = L;
@@ -1056,7 +1017,7 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
   const int64_t stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
   // Header row of each tile: int32 {pass-1 terminal edge, end state, ...}.
   const int64_t hstride = stride / 4;
-  int32_t* hdr = reinterpret_cast<int32_t*>(temp_edges + (int64_t)L * lay.row_bytes);
+  int32_t* hdr = reinterpret_cast<int32_t*>(temp_edges + exl3::header_offset(lay, L));
   int32_t* best_edges = hdr + exl3::HDR_BEST_EDGE;
   int32_t* end_states = hdr + exl3::HDR_END_STATE;
   const int64_t cap = (wave_cap > 0) ? std::min(batch_cap, wave_cap) : batch_cap;
@@ -1066,11 +1027,12 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
   for (int64_t off = 0; off < n; off += chunk_max) {
     const int chunk = (int)std::min<int64_t>(chunk_max, n - off);
     FwdArgs a = forward_args(in + off * L, chunk, K, cb, L, temp_edges, temp_costs);
-    // Pass 1: rotation L/2, unconstrained. The traceback reads ring rows
-    // 0..L/2-1 only, i.e. forward steps L/2..L-1 (reference_encoder.py:284-288).
+    // Pass 1: rotation L/2, unconstrained. The traceback covers ring rows
+    // 0..L/2-1 only, i.e. forward steps L/2..L-1 (reference_encoder.py:284-288),
+    // so only those backpointer rows and the cost rows they need are stored.
     a.roll = L / 2;
     a.store_rows = L / 2;
-    a.store_from = exl3::first_needed_row(K, L);
+    a.store_from = exl3::first_needed_row(lay, L);
     a.cost_slot = 0;
     a.best_edges = best_edges;
     a.best_stride = hstride;

@@ -14,9 +14,10 @@ is no CPU fallback.
 
 Deviations from the reference, all deliberate:
 
-* scratch layout: ``temp_edges`` is ``uint8 (B, L+1, ROW)``: K-bit
-  backpointer rows (K = 1, 2, 8) or fp16 cost rows (K = 3..7), see
-  include/exl3_encoder.h; sized by the new ScratchEstimator;
+* scratch layout: ``temp_edges`` is ``uint8 (B, ROWS, ROW)``: every
+  stride-th fp16 cost row (K = 1..7) or one backpointer byte per edge
+  (K = 8), plus a header row, see include/exl3_encoder.h; sized by the new
+  ScratchEstimator;
 * the arena's default batch capacity is 4096 tiles (the reference used 64 for
   the Arc iGPU), enough for eight waves of 1024-thread workgroups on 256 CUs;
 * traceback placement: ``gpu_resident`` runs the fused encoder;
@@ -43,7 +44,7 @@ from . import build as _build
 from ._native import QuantizeExtension, load_library
 from .memory_policy import MemoryPolicy, MemoryPressureError, capture_snapshot
 from .reference_encoder import EncodingResult
-from .scratch_estimator import ScratchEstimator, backpointer_row_bytes
+from .scratch_estimator import ScratchEstimator, backpointer_row_bytes, tile_rows
 from .trellis_format import (CB_3INST, CB_MCG, CB_MUL1, codebook_lut, tensor_core_perm,
                              tensor_core_perm_inv)
 
@@ -253,7 +254,8 @@ class ScratchArena:
                     allocator_hook(cand_b)
                 dev = f"cuda:{self.device_index}"
                 costs = torch.empty((cand_b, 2, est.states), dtype=torch.float16, device=dev)
-                edges = torch.empty((cand_b, tile_len + 1, rb), dtype=torch.uint8, device=dev)
+                edges = torch.empty((cand_b, tile_rows(k, tile_len), rb), dtype=torch.uint8,
+                                    device=dev)
                 post = capture_snapshot(self.device_index)
                 self.policy.check_after_commit(post, pre_snapshot=snap,
                                                expected_bytes=est.total_bytes,

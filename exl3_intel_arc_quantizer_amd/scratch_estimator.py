@@ -1,20 +1,22 @@
-"""Scratch sizing for the MI355X encoder (K-bit backpointer / cost-row layout).
+"""Scratch sizing for the MI355X encoder (cost-row / backpointer layout).
 
 Counterpart of exl3_quant/scratch_estimator.py:23-172 with the same class
 and method names. The formula changes with the layout
-(include/exl3_encoder.h):
+(include/exl3_encoder.h, csrc/exl3_layout.h):
 
     S      = 65536 >> K                      edges per step
-    row    = S * BPB / 8                     K = 1, 2, 8: K-bit backpointer rows
-                                             (BPB = K rounded up to 1, 2, 4, 8)
-           = S * 2                           K = 3..7: fp16 cost rows
+    row    = S * 2                           K = 1..7: fp16 cost rows
+           = S                               K = 8: one backpointer byte per edge
+    rows   = (T - 2) // stride + 2           K = 1..7: every stride-th step
+                                             (stride 8, 4, 2, 2, 2, 1, 1) + header
+           = T + 1                           K = 8: T ring rows + header
     costs  = B * 2 * S * 2                   terminal fp16 costs of both passes
-    edges  = B * (T + 1) * row               T rows + one header row per tile
+    edges  = B * rows * row
 
 The reference's int16 layout, ``B * T * S * 2``, is still available by
 passing ``bytes_per_edge`` explicitly (e.g. to compare the two). Per tile at
-T = 256: K=2 1.0 MiB (reference 8 MiB), K=3 4.0 MiB (4 MiB), K=4 2.0 MiB
-(2 MiB), K=6 514 KiB (512 KiB).
+T = 256: K=1 2.06 MiB (reference 16 MiB), K=2 2.03 MiB (8 MiB), K=3 2.02 MiB
+(4 MiB), K=4 1.01 MiB (2 MiB), K=5 516 KiB (1 MiB), K=6 514 KiB (512 KiB).
 """
 
 from __future__ import annotations
@@ -32,20 +34,30 @@ BYTES_PER_GB = 1000 ** 3
 
 
 def uses_cost_rows(k: int) -> bool:
-    """K = 3..7 keep fp16 cost rows; K = 1, 2, 8 keep K-bit backpointers."""
-    return 3 <= k <= 7
+    """K = 1..7 keep fp16 cost rows; K = 8 keeps one backpointer byte per edge."""
+    return 1 <= k <= 7
+
+
+def row_stride(k: int) -> int:
+    """Steps between stored cost rows (exl3_layout.h row_stride)."""
+    return {1: 8, 2: 4, 3: 2, 4: 2, 5: 2}.get(k, 1)
 
 
 def backpointer_bits(k: int) -> int:
     """Bits stored per edge and row (exl3_layout.h make_layout)."""
-    if uses_cost_rows(k):
-        return 16
-    return 8 if k == 8 else k
+    return 16 if uses_cost_rows(k) else 8
 
 
 def backpointer_row_bytes(k: int) -> int:
     """Bytes of one scratch row (exl3_scratch_row_bytes)."""
     return (65536 >> k) * backpointer_bits(k) // 8
+
+
+def tile_rows(k: int, t: int = 256) -> int:
+    """Scratch rows per tile, header included (exl3_layout.h tile_rows)."""
+    if uses_cost_rows(k):
+        return (t - 2) // row_stride(k) + 2
+    return t + 1
 
 
 @dataclass(frozen=True)
@@ -101,8 +113,8 @@ class ScratchEstimator:
     def estimate_scratch(cls, k: int, t: int = 256, b: int = 256, bytes_per_cost: int = 2,
                          bytes_per_edge: Optional[int] = None) -> ScratchAllocation:
         """Scratch bytes for ``b`` tiles of length ``t``. ``bytes_per_edge=None``
-        selects the K-bit layout of this encoder; an explicit value reproduces
-        the reference's ``b*t*S*bytes_per_edge`` formula."""
+        selects the layout of this encoder; an explicit value reproduces the
+        reference's ``b*t*S*bytes_per_edge`` formula."""
         if b <= 0:
             raise ValueError(f"Batch size B must be positive, got {b}")
         if t <= 0:
@@ -113,7 +125,7 @@ class ScratchEstimator:
             if k > 8:
                 raise ValueError(f"the encoder supports K in 1..8, got {k}")
             bits = backpointer_bits(k)
-            edges_bytes = b * (t + 1) * backpointer_row_bytes(k)
+            edges_bytes = b * tile_rows(k, t) * backpointer_row_bytes(k)
         else:
             bits = 8 * bytes_per_edge
             edges_bytes = b * t * states * bytes_per_edge

@@ -143,7 +143,7 @@ def test_other_golden_sets(name):
 
 
 def _pred_table(temp_edges_row_block, K, L):
-    """Decode one tile's K-bit backpointer rows into the reference's
+    """Decode one tile's backpointer rows (K = 8) into the reference's
     predecessor-edge table (L, E) uint16."""
     from exl3_intel_arc_quantizer_amd import _native
     from exl3_intel_arc_quantizer_amd.scratch_estimator import backpointer_bits
@@ -162,13 +162,13 @@ def _pred_table(temp_edges_row_block, K, L):
 @pytest.mark.parametrize("generic", [False, True])
 def test_forward_pass_pins(ext, torch_mod, generic):
     """Split forward pass (quantize_xpu.cpp:169-215) against the reference's
-    forward(): terminal costs bit-exact; in backpointer mode (K = 1, 2, 8) the
-    full predecessor table against its hash; in cost-row mode (K = 3..7) every
-    stored cost row (even steps only at K = 3..5, group-major positions)
-    against the C oracle's per-step costs. Then the split backward pass, which
-    recomputes the odd rows, reaches the reference's end state."""
-    from exl3_intel_arc_quantizer_amd._native import load_library, row_bytes
-    from exl3_intel_arc_quantizer_amd.scratch_estimator import uses_cost_rows
+    forward(): terminal costs bit-exact; in cost-row mode (K = 1..7) every
+    stored cost row (every stride-th step, group-major positions) against
+    the C oracle's per-step costs; in backpointer mode (K = 8) the full
+    predecessor table against its hash. Then the split backward pass, which
+    rebuilds the unstored steps, reaches the reference's end state."""
+    from exl3_intel_arc_quantizer_amd._native import edges_shape, load_library
+    from exl3_intel_arc_quantizer_amd.scratch_estimator import row_stride, uses_cost_rows
     g = load_golden("forward_pass")
     for i in range(4):
         K, roll, pre, best, end = (int(v) for v in g[f"case{i}_meta"])
@@ -176,9 +176,8 @@ def test_forward_pass_pins(ext, torch_mod, generic):
         tile16 = g[f"case{i}_tile"].view(np.float16)
         x = torch_mod.from_numpy(tile16.astype(np.float32)).cuda().reshape(1, 256)
         E = 65536 >> K
-        rb = row_bytes(K)
         costs = torch_mod.zeros((1, 2, E), dtype=torch_mod.float16, device="cuda")
-        edges = torch_mod.zeros((1, 257, rb), dtype=torch_mod.uint8, device="cuda")
+        edges = torch_mod.zeros(edges_shape(1, K), dtype=torch_mod.uint8, device="cuda")
         pre_t = torch_mod.full((1,), pre, dtype=torch_mod.int32, device="cuda")
         ext.quantize_tiles_forward_pass(x, costs, edges, pre_t, K, False, True, roll, 1, 32,
                                         generic)
@@ -194,15 +193,14 @@ def test_forward_pass_pins(ext, torch_mod, generic):
         if uses_cost_rows(K):
             _, _, want_rows = c_oracle.forward_pass(tile16, K=K, cb=2, roll=roll, pre_state=pre,
                                                     with_rows=True)
-            got_rows = block[:255].view(np.uint16).reshape(255, E)
             lib = load_library()
             pos = np.array([lib.exl3_backpointer_slot(K, e) for e in range(E)], dtype=np.int64)
-            sparse = 3 <= K <= 5
-            for r in range(255):
-                if sparse and r % 2:
-                    continue
-                np.testing.assert_array_equal(got_rows[r][pos], want_rows[r], err_msg=f"row {r}")
-            hdr = block[256]
+            stride = row_stride(K)
+            assert block.shape[0] == 254 // stride + 2
+            for r in range(0, 255, stride):
+                got = block[r // stride].view(np.uint16)
+                np.testing.assert_array_equal(got[pos], want_rows[r], err_msg=f"row {r}")
+            hdr = block[-1]
             np.testing.assert_array_equal(hdr[16:16 + 512].view(np.uint16), tile16.view(np.uint16))
             assert int(hdr[8:12].view(np.int32)[0]) == pre
         else:
@@ -210,6 +208,28 @@ def test_forward_pass_pins(ext, torch_mod, generic):
             np.testing.assert_array_equal(table[:4, :64], g[f"case{i}_edges_head"])
             assert hashlib.sha256(table.tobytes()).hexdigest() == str(g[f"case{i}_edges_sha256"])
         assert int(ends.item()) == end
+
+
+def test_backpointer_rows_k8(ext, torch_mod):
+    """K = 8 keeps one backpointer byte per edge and ring row: the decoded
+    predecessor table and terminal costs of a forward pass equal the C
+    oracle's (reference forward(), reference_encoder.py:130-204), for an
+    unconstrained and a constrained pass."""
+    from exl3_intel_arc_quantizer_amd._native import edges_shape
+    rng = np.random.default_rng(88)
+    tile16 = rng.normal(0.0, 1.1, size=256).astype(np.float16)
+    x = torch_mod.from_numpy(tile16.astype(np.float32)).cuda().reshape(1, 256)
+    for roll, pre in ((128, -1), (0, 77)):
+        print(f"K=8 forward roll={roll} pre={pre}", flush=True)
+        costs = torch_mod.zeros((1, 2, 256), dtype=torch_mod.float16, device="cuda")
+        edges = torch_mod.zeros(edges_shape(1, 8), dtype=torch_mod.uint8, device="cuda")
+        pre_t = torch_mod.full((1,), pre, dtype=torch_mod.int32, device="cuda")
+        ext.quantize_tiles_forward_pass(x, costs, edges, pre_t, 8, False, True, roll, 0)
+        torch_mod.cuda.synchronize()
+        want_edges, want_costs = c_oracle.forward_pass(tile16, K=8, cb=2, roll=roll, pre_state=pre)
+        np.testing.assert_array_equal(_pred_table(edges[0].cpu().numpy(), 8, 256), want_edges)
+        np.testing.assert_array_equal(costs[0, 0].cpu().numpy().view(np.uint16),
+                                      want_costs.view(np.uint16))
 
 
 def test_traceback_modes_and_variants_agree():
@@ -257,13 +277,13 @@ def test_queue_ordering_and_async(ext, torch_mod):
     on the same stream, no host sync in between."""
     rng = np.random.default_rng(808)
     raw = rng.normal(0.0, 0.5, size=(4, 256)).astype(np.float16).astype(np.float32)
-    from exl3_intel_arc_quantizer_amd._native import row_bytes
+    from exl3_intel_arc_quantizer_amd._native import edges_shape
     in_t = torch_mod.from_numpy(raw).cuda()
     in_t.mul_(2.0)
     out_w = torch_mod.empty_like(in_t)
     out_i = torch_mod.empty((4, 256), dtype=torch_mod.int16, device="cuda")
     costs = torch_mod.empty((4, 2, 8192), dtype=torch_mod.float16, device="cuda")
-    edges = torch_mod.empty((4, 257, row_bytes(3)), dtype=torch_mod.uint8, device="cuda")
+    edges = torch_mod.empty(edges_shape(4, 3), dtype=torch_mod.uint8, device="cuda")
     ext.quantize_tiles(in_t, out_w, out_i, costs, edges, 3, False, True)
     out_w.add_(1.0)
     torch_mod.cuda.synchronize()
@@ -275,18 +295,18 @@ def test_queue_ordering_and_async(ext, torch_mod):
 
 def test_extension_rejects_malformed_tensors(ext, torch_mod):
     """tests/test_xpu_quantizer.py:260-269."""
-    from exl3_intel_arc_quantizer_amd._native import row_bytes
+    from exl3_intel_arc_quantizer_amd._native import edges_shape
     in_t = torch_mod.zeros((1, 256), dtype=torch_mod.float32, device="cuda")
     out_w = torch_mod.zeros((1, 256), dtype=torch_mod.float32, device="cuda")
     out_i = torch_mod.zeros((1, 256), dtype=torch_mod.int16, device="cuda")
     costs = torch_mod.zeros((1, 2, 16384), dtype=torch_mod.float16, device="cuda")
-    edges = torch_mod.zeros((1, 257, row_bytes(2)), dtype=torch_mod.uint8, device="cuda")
+    edges = torch_mod.zeros(edges_shape(1, 2), dtype=torch_mod.uint8, device="cuda")
     with pytest.raises(RuntimeError):
         ext.quantize_tiles(in_t, out_w, out_i, costs, edges, 2, True, True)
     with pytest.raises(RuntimeError):
         ext.quantize_tiles(in_t.cpu(), out_w, out_i, costs, edges, 2, False, True)
     with pytest.raises(RuntimeError):
-        ext.quantize_tiles(in_t, out_w, out_i, costs, edges[:, :256], 2, False, True)
+        ext.quantize_tiles(in_t, out_w, out_i, costs, edges[:, :-1], 2, False, True)
     with pytest.raises(RuntimeError):
         ext.quantize_tiles(in_t, out_w, out_i.float(), costs, edges, 2, False, True)
 

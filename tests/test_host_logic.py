@@ -29,10 +29,12 @@ def test_reference_formula_fixtures_still_reproducible():
         assert a.costs_mib == pytest.approx(costs_mib)
 
 
-@pytest.mark.parametrize("k,per_tile", [(1, 257 * 4096), (2, 257 * 4096), (3, 257 * 16384),
-                                        (4, 257 * 8192), (5, 257 * 4096), (6, 257 * 2048),
-                                        (7, 257 * 1024), (8, 257 * 256)])
-def test_kbit_layout_formula(k, per_tile):
+# Stored cost rows (every stride-th of steps 0..254) plus the header row, of
+# E * 2 bytes; K = 8: 256 ring rows plus the header, E bytes each.
+@pytest.mark.parametrize("k,per_tile", [(1, 33 * 65536), (2, 65 * 32768), (3, 129 * 16384),
+                                        (4, 129 * 8192), (5, 129 * 4096), (6, 256 * 2048),
+                                        (7, 256 * 1024), (8, 257 * 256)])
+def test_layout_formula(k, per_tile):
     a = ScratchEstimator.estimate_scratch(k=k, t=256, b=10)
     assert a.edges_bytes == 10 * per_tile
     assert a.costs_bytes == 10 * 2 * (65536 >> k) * 2
@@ -48,13 +50,13 @@ def test_estimator_validation_and_max_batch():
         ScratchEstimator.estimate_scratch(k=3, b=0)
     with pytest.raises(ValueError):
         ScratchEstimator.estimate_scratch(k=3, t=-1)
-    # 288 GB HBM, 8 GiB reserve, K=2: ~1.06 MiB per tile.
+    # 288 GB HBM, 8 GiB reserve, K=2: ~2.1 MiB per tile.
     max_b, alloc = ScratchEstimator.calculate_max_batch_size(k=2, available_vram_bytes=288 * 10 ** 9)
     assert alloc.total_bytes <= 288 * 10 ** 9 - 8 * BYTES_PER_GIB
-    assert max_b == (288 * 10 ** 9 - 8 * BYTES_PER_GIB) // (257 * 4096 + 2 * 16384 * 2)
+    assert max_b == (288 * 10 ** 9 - 8 * BYTES_PER_GIB) // (65 * 32768 + 2 * 16384 * 2)
     max_b, _ = ScratchEstimator.calculate_max_batch_size(
         k=3, available_vram_bytes=64 * BYTES_PER_GIB, max_single_alloc_bytes=16 * BYTES_PER_MIB)
-    assert max_b == 16 * BYTES_PER_MIB // (257 * 16384)
+    assert max_b == 16 * BYTES_PER_MIB // (129 * 16384)
     with pytest.raises(ValueError):
         ScratchEstimator.calculate_max_batch_size(k=2, available_vram_bytes=BYTES_PER_GIB)
 
