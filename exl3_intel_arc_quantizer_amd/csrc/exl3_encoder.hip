@@ -296,9 +296,10 @@ __device__ __forceinline__ u16x2 quad_min_u16x2(u16x2 v) {
 // into the running minimum (costs are non-negative fp16 with no NaN, where
 // IEEE minimum returns the same bits as an integer minimum). The pair minima
 // are in edge order for 32-bit LDS stores. CB is the codebook selector
-// (compile time keeps the prologue's registers low).
+// (compile time keeps the prologue's registers low). Eight waves per SIMD:
+// two workgroups per CU where LDS allows (K >= 2), which caps VGPRs at 64.
 template <int K, int G, int J, int P, int CB>
-__global__ void __launch_bounds__(1024) acs_forward_rows(FwdArgs a) {
+__global__ void __launch_bounds__(1024, 8) acs_forward_rows(FwdArgs a) {
   using C = FastCfg<K, G, J, P>;
   constexpr int JP = J / 2;
   static_assert(C::Q % 2 == 0, "branches are folded two at a time");
