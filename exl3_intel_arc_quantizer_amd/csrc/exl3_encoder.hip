@@ -135,13 +135,23 @@ __device__ __forceinline__ uint32_t wave_min(uint32_t v) {
   return v;
 }
 
+// LDS position of edge x in a padded cost vector: PAD elements after every
+// block of 2^KS edges (KS = 16 - 2K, one block per branch k of x = (k << KS)
+// | h). The padding skews the blocks over the LDS banks, so gathering one
+// group's 2^K costs (one edge per block) is conflict-free.
+template <int KS, int PAD>
+__device__ __forceinline__ int lds_pos(int x) {
+  return PAD ? x + (x >> KS) * PAD : x;
+}
+
 // Lowest-index minimum of the terminal costs (reference argmin_cost,
 // reference_encoder.py:206-214): key = cost_bits << 16 | edge; all +inf
 // gives edge 0. Result broadcast to all threads via s_red[0].
-template <int NT>
+template <int NT, int KS = 0, int PAD = 0>
 __device__ uint32_t block_argmin(const uint16_t* cost, int E, uint32_t* s_red) {
   uint32_t best = 0xFFFFFFFFu;
-  for (int e = threadIdx.x; e < E; e += NT) best = umin(best, ((uint32_t)cost[e] << 16) | (uint32_t)e);
+  for (int e = threadIdx.x; e < E; e += NT)
+    best = umin(best, ((uint32_t)cost[lds_pos<KS, PAD>(e)] << 16) | (uint32_t)e);
   best = wave_min(best);
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) s_red[wave] = best;
@@ -175,7 +185,7 @@ struct FwdArgs {
 
 // Load the tile's fp16 inputs into LDS, record pre_state (and, for cost rows,
 // the inputs) in the tile header, and set the initial cost vector.
-template <int NT>
+template <int NT, int KS = 0, int PAD = 0>
 __device__ __forceinline__ void forward_prologue(const FwdArgs& a, int E, bool stash_inputs,
                                                  f16* s_w, uint16_t* cost0, int& pre_out) {
   const int tile = blockIdx.x;
@@ -188,21 +198,22 @@ __device__ __forceinline__ void forward_prologue(const FwdArgs& a, int E, bool s
   }
   const int pre = a.pre_states ? a.pre_states[(int64_t)tile * a.pre_stride] : -1;
   if (threadIdx.x == 0) reinterpret_cast<int32_t*>(hdr)[exl3::HDR_PRE_STATE] = pre;
-  for (int e = threadIdx.x; e < E; e += NT) cost0[e] = (pre < 0 || e == pre) ? 0 : 0x7C00;
+  for (int e = threadIdx.x; e < E; e += NT)
+    cost0[lds_pos<KS, PAD>(e)] = (pre < 0 || e == pre) ? 0 : 0x7C00;
   pre_out = pre;
 }
 
 // Terminal costs to temp_costs and the pass-1 terminal argmin.
-template <int NT>
+template <int NT, int KS = 0, int PAD = 0>
 __device__ __forceinline__ void forward_epilogue(const FwdArgs& a, int E, const uint16_t* cfin,
                                                  uint32_t* s_red) {
   const int tile = blockIdx.x;
   if (a.term_costs) {
     uint16_t* dst = a.term_costs + ((int64_t)tile * 2 + a.cost_slot) * E;
-    for (int e = threadIdx.x; e < E; e += NT) dst[e] = cfin[e];
+    for (int e = threadIdx.x; e < E; e += NT) dst[e] = cfin[lds_pos<KS, PAD>(e)];
   }
   if (a.best_edges) {
-    const uint32_t b = block_argmin<NT>(cfin, E, s_red);
+    const uint32_t b = block_argmin<NT, KS, PAD>(cfin, E, s_red);
     if (threadIdx.x == 0) a.best_edges[(int64_t)tile * a.best_stride] = (int32_t)b;
   }
 }
@@ -213,7 +224,7 @@ __device__ __forceinline__ void forward_epilogue(const FwdArgs& a, int E, const 
 // positions 8c .. 8c + 7, gathered from LDS; the global stores stay
 // contiguous. The chunks go to the first E / 8 threads: leaving the other
 // waves free measured faster than spreading the gather over every wave.
-template <int NT>
+template <int NT, int KS = 0, int PAD = 0>
 __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const uint16_t* src,
                                                int step) {
   const BpLayout lay = exl3::make_layout(K);
@@ -227,8 +238,8 @@ __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const ui
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int t0 = 8 * c + 2 * m, t1 = t0 + 1;
-      const uint32_t lo = src[((t0 & ((1 << K) - 1)) << ks) | (t0 >> K)];
-      const uint32_t hi = src[((t1 & ((1 << K) - 1)) << ks) | (t1 >> K)];
+      const uint32_t lo = src[lds_pos<KS, PAD>(((t0 & ((1 << K) - 1)) << ks) | (t0 >> K))];
+      const uint32_t hi = src[lds_pos<KS, PAD>(((t1 & ((1 << K) - 1)) << ks) | (t1 >> K))];
       v[m] = lo | (hi << 16);
     }
     dst[c] = make_uint4(v[0], v[1], v[2], v[3]);
@@ -297,13 +308,20 @@ __device__ __forceinline__ u16x2 quad_min_u16x2(u16x2 v) {
 // IEEE minimum returns the same bits as an integer minimum). The pair minima
 // are in edge order for 32-bit LDS stores. CB is the codebook selector
 // (compile time keeps the prologue's registers low). Eight waves per SIMD:
-// two workgroups per CU where LDS allows (K >= 2), which caps VGPRs at 64.
+// two workgroups per CU where LDS allows (K >= 2), which caps VGPRs at 64;
+// K = 1 needs 128 KiB of LDS and runs one workgroup per CU.
 template <int K, int G, int J, int P, int CB>
-__global__ void __launch_bounds__(1024, 8) acs_forward_rows(FwdArgs a) {
+__global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdArgs a) {
   using C = FastCfg<K, G, J, P>;
   constexpr int JP = J / 2;
+  constexpr int KS = 16 - 2 * K;
+  constexpr int PAD = K >= 6 ? 2 : 0;               // one dword per branch block (measured
+                                                    // a loss at K <= 5)
+  constexpr int SP = C::S + PAD;                    // padded block stride
+  constexpr int EP = C::E + (1 << K) * PAD;         // padded vector length
   static_assert(C::Q % 2 == 0, "branches are folded two at a time");
-  __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][C::E];
+  static_assert(PAD == 0 || G == 1, "padding keeps group pairs of G > 1 together");
+  __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][EP];
   __shared__ f16 s_w[256];
   __shared__ uint32_t s_red[16];
 
@@ -329,7 +347,7 @@ __global__ void __launch_bounds__(1024, 8) acs_forward_rows(FwdArgs a) {
         cbv[g][jp][q] = v;
       }
   int pre;
-  forward_prologue<C::NT>(a, C::E, true, s_w, s_cost[0], pre);
+  forward_prologue<C::NT, KS, PAD>(a, C::E, true, s_w, s_cost[0], pre);
   __syncthreads();
 
   for (int i = 0; i < L; ++i) {
@@ -337,7 +355,7 @@ __global__ void __launch_bounds__(1024, 8) acs_forward_rows(FwdArgs a) {
     if (ri >= L) ri -= L;
     const uint16_t* cin = s_cost[i & 1];
     uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[(i & 1) ^ 1]);
-    if (stores_row(a, K, i)) store_cost_row<C::NT>(a, K, cin, i - 1);
+    if (stores_row(a, K, i)) store_cost_row<C::NT, KS, PAD>(a, K, cin, i - 1);
     const f16 w = s_w[ri];
     f16x2 w2;
     w2.x = w;
@@ -352,7 +370,7 @@ __global__ void __launch_bounds__(1024, 8) acs_forward_rows(FwdArgs a) {
       uint32_t cw[2][(G + 1) / 2];
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
-        const uint16_t* src = cin + (k + b * P) * C::S + h0;
+        const uint16_t* src = cin + (k + b * P) * SP + h0;
         if constexpr (G == 1) {
           cw[b][0] = src[0];
         } else {
@@ -387,11 +405,11 @@ __global__ void __launch_bounds__(1024, 8) acs_forward_rows(FwdArgs a) {
       for (int jp = 0; jp < JP; ++jp) {
         const u16x2 v = quad_min_u16x2<P>(__builtin_bit_cast(u16x2, m[g][jp]));
         const int e = ((h0 + g) << K) | (jj * J + 2 * jp);
-        if (P == 1 || p == 0) cout[e >> 1] = __builtin_bit_cast(uint32_t, v);
+        if (P == 1 || p == 0) cout[lds_pos<KS, PAD>(e) >> 1] = __builtin_bit_cast(uint32_t, v);
       }
     __syncthreads();
   }
-  forward_epilogue<C::NT>(a, C::E, s_cost[L & 1], s_red);
+  forward_epilogue<C::NT, KS, PAD>(a, C::E, s_cost[L & 1], s_red);
 }
 
 // --------------------------------------------------------- generic kernel
@@ -710,77 +728,86 @@ __global__ void prepare_kernel(const float* __restrict__ raw, float* __restrict_
   out[idx] = (float)(f16)v;
 }
 
-// numpy float32 pairwise summation of a block of n in [8, 128] elements
-// (eight accumulators, numpy/_core/src/umath/loops_utils.h.src).
-__device__ float pairwise_block(const float* a, int n) {
-  float r[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = a[j];
-  int i = 8;
-  for (; i < n - (n % 8); i += 8)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] += a[i + j];
-  float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-  for (; i < n; ++i) res += a[i];
-  return res;
+// numpy float32 pairwise summation (numpy/_core/src/umath/loops_utils.h.src)
+// of a block of n in [8, 128] elements from LDS, by the wave: lane j < 8
+// accumulates r[j] = a[j] + a[j + 8] + ... in order, the tail n % 8 is
+// added after ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)); the xor
+// butterfly forms exactly those sums (fp32 addition is commutative). The
+// result is valid in lane 0.
+__device__ __forceinline__ float pairwise_block_wave(const float* a, int n, int lane) {
+  float r = 0.0f;
+  if (lane < 8) {
+    r = a[lane];
+    for (int i = 8; i < n - (n % 8); i += 8) r += a[i + lane];
+  }
+  r += __shfl_xor(r, 1, 64);
+  r += __shfl_xor(r, 2, 64);
+  r += __shfl_xor(r, 4, 64);
+  for (int i = n - (n % 8); i < n; ++i) r += a[i];
+  return r;
 }
 
 // np.sum over n in [16, 256] float32 values: 0 + pairwise(n) where blocks
-// above 128 split at (n/2 rounded down to a multiple of 8).
-__device__ float numpy_sum_f32(const float* a, int n) {
-  if (n <= 128) return 0.0f + pairwise_block(a, n);
+// above 128 split at n/2 rounded down to a multiple of 8.
+__device__ __forceinline__ float numpy_sum_f32_wave(const float* a, int n, int lane) {
+  if (n <= 128) return 0.0f + pairwise_block_wave(a, n, lane);
   int n2 = n / 2;
   n2 -= n2 % 8;
-  return 0.0f + (pairwise_block(a, n2) + pairwise_block(a + n2, n - n2));
+  const float lo = pairwise_block_wave(a, n2, lane);
+  const float hi = pairwise_block_wave(a + n2, n - n2, lane);
+  return 0.0f + (lo + hi);
 }
 
-__global__ void finalize_kernel(const float* __restrict__ x, const float* __restrict__ raw,
-                                const float* __restrict__ out_w,
-                                const int16_t* __restrict__ out_idx, uint16_t* __restrict__ packed,
-                                float* __restrict__ path_cost, float* __restrict__ distortion,
-                                uint16_t* __restrict__ recon_orig, int64_t n, int K, int L,
-                                int permuted) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n) return;
+// One wave per tile: path cost, distortion, original-order reconstruction
+// and packing (reference_encoder.py:296-316, xpu_quantizer.py:933-976).
+__global__ void __launch_bounds__(64) finalize_kernel(
+    const float* __restrict__ x, const float* __restrict__ raw, const float* __restrict__ out_w,
+    const int16_t* __restrict__ out_idx, uint16_t* __restrict__ packed,
+    float* __restrict__ path_cost, float* __restrict__ distortion,
+    uint16_t* __restrict__ recon_orig, int K, int L, int permuted) {
+  __shared__ f16 s_dh[256];
+  __shared__ float s_sq[256];
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x;
   const float* xt = x + t * L;
   const float* wt = out_w + t * L;
   const int16_t* it = out_idx + t * L;
 
-  // Path cost along the chosen states in ring order (xpu_quantizer.py:933-941).
-  f16 acc = 0;
-  for (int i = 0; i < L; ++i) {
-    const f16 dh = (f16)wt[i] - (f16)xt[i];
-    acc = __builtin_fmaf16(dh, dh, i == 0 ? (f16)0 : acc);
-  }
-  path_cost[t] = (float)acc;
-
-  // Squared error in evaluation order (reference_encoder.py:302-311).
-  float sq[256];
-  for (int pidx = 0; pidx < L; ++pidx) {
-    const int src = permuted ? tc_perm_inv(pidx) : pidx;
+  for (int i = lane; i < L; i += 64) {
+    s_dh[i] = (f16)wt[i] - (f16)xt[i];
+    // Squared error in evaluation order (reference_encoder.py:302-311).
+    const int src = permuted ? tc_perm_inv(i) : i;
     const f16 rec = (f16)wt[src];
-    if (recon_orig) recon_orig[t * L + pidx] = bits_f16(rec);
-    const float orig = permuted ? raw[t * L + pidx] : xt[pidx];
+    if (recon_orig) recon_orig[t * L + i] = bits_f16(rec);
+    const float orig = permuted ? raw[t * L + i] : xt[i];
     const float d = orig - (float)rec;
-    sq[pidx] = d * d;
+    s_sq[i] = d * d;
   }
-  distortion[t] = numpy_sum_f32(sq, L);
+  __syncthreads();
 
-  // pack_trellis + swap16_storage (trellis_format.py:120-174).
-  if (packed && L == 256) {
+  const float dist = numpy_sum_f32_wave(s_sq, L, lane);
+  if (lane == 0) {
+    distortion[t] = dist;
+    // Path cost along the chosen states in ring order (xpu_quantizer.py:933-941).
+    f16 acc = __builtin_fmaf16(s_dh[0], s_dh[0], (f16)0);
+    for (int i = 1; i < L; ++i) acc = __builtin_fmaf16(s_dh[i], s_dh[i], acc);
+    path_cost[t] = (float)acc;
+  }
+
+  // pack_trellis + swap16_storage (trellis_format.py:120-174): one span per lane.
+  if (packed && L == 256 && lane < 16) {
     uint16_t* o = packed + t * 16 * K;
-    for (int span = 0; span < 16; ++span) {
-      uint32_t buf = 0;
-      int held = 32, j = span * K;
-      for (int e = 0; e < 16; ++e) {
-        held -= K;
-        buf |= ((uint32_t)(uint16_t)it[span * 16 + e] & ((1u << K) - 1u)) << held;
-        if (held <= 16) {
-          o[j ^ 1] = (uint16_t)(buf >> 16);  // j ^ 1: half-word swap of each pair
-          buf <<= 16;
-          held += 16;
-          ++j;
-        }
+    const int span = lane;
+    uint32_t buf = 0;
+    int held = 32, j = span * K;
+    for (int e = 0; e < 16; ++e) {
+      held -= K;
+      buf |= ((uint32_t)(uint16_t)it[span * 16 + e] & ((1u << K) - 1u)) << held;
+      if (held <= 16) {
+        o[j ^ 1] = (uint16_t)(buf >> 16);  // j ^ 1: half-word swap of each pair
+        buf <<= 16;
+        held += 16;
+        ++j;
       }
     }
   }
@@ -1081,10 +1108,9 @@ int exl3_finalize_tiles(const float* x, const float* raw, const float* out_w,
   if (n <= 0 || K < 1 || K > 8 || (L != 256 && L != 160)) return set_error("bad finalize shape");
   if (permuted && (L != 256 || !raw)) return set_error("permuted finalize needs L=256 raw tiles");
   if (!x || !out_w || !out_idx || !path_cost || !distortion) return set_error("NULL buffer");
-  const int block = 64;
-  hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)((n + block - 1) / block)), dim3(block), 0,
-                     as_stream(stream), x, raw, out_w, out_idx, packed, path_cost, distortion,
-                     recon_orig, n, K, L, permuted);
+  if (n > INT32_MAX) return set_error("too many tiles for one finalize launch");
+  hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)n), dim3(64), 0, as_stream(stream), x, raw,
+                     out_w, out_idx, packed, path_cost, distortion, recon_orig, K, L, permuted);
   return check_launch("finalize_tiles");
 }
 
