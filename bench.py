@@ -190,7 +190,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the encoder "
-              "shards by tiles across GPUs, see DESIGN.md", file=sys.stderr)
+              "would shard by tiles (each GPU a contiguous slice of the batch, outputs gathered "
+              "once)", file=sys.stderr)
         return 2
 
     import torch

@@ -274,6 +274,71 @@ class QuantizeExtension:
                 int(roll), int(cost_slot), int(bool(write_output)), _stream(dev)),
                 "quantize_tiles_backward_pass")
 
+    # quantize_xpu.cpp:261-300, quantize_kernels.sycl:756-841
+    def quantize_tiles_usm_host(self, input_tiles, temp_costs, output_tiles_cpu,
+                                output_indices_cpu, lut_cpu, K: int, mcg: bool, mul1: bool,
+                                sg_size: int = 32) -> list:
+        """The reference's host-visible-edges variant: states and codebook
+        values land in CPU tensors, and [search_s, trace_s] is returned. On
+        MI355X the search and the traceback both run on the GPU (split
+        forward/backward passes over an internal device scratch of
+        temp_costs' batch size); the results are copied to the CPU tensors.
+        ``lut_cpu`` is validated as in the reference and otherwise unused:
+        the GPU decodes states in registers."""
+        torch = _torch()
+        cb = _resolve_cb(mcg, mul1)
+        dev = _check_device_tensor(input_tiles, "input_tiles", torch.float32, 2)
+        if _check_device_tensor(temp_costs, "temp_costs", torch.float16, 3) != dev:
+            raise RuntimeError("temp_costs must be on the same GPU device")
+        if not (output_tiles_cpu.device.type == "cpu" and output_tiles_cpu.is_contiguous()
+                and output_tiles_cpu.dtype == torch.float32):
+            raise RuntimeError("output_tiles_cpu must be a contiguous float32 CPU tensor")
+        if not (output_indices_cpu.device.type == "cpu" and output_indices_cpu.is_contiguous()
+                and output_indices_cpu.dtype == torch.int16):
+            raise RuntimeError("output_indices_cpu must be a contiguous int16 CPU tensor")
+        if not (lut_cpu.device.type == "cpu" and lut_cpu.is_contiguous()
+                and lut_cpu.dtype == torch.float32 and lut_cpu.numel() == 65536):
+            raise RuntimeError("lut_cpu must be a 65536-element float32 CPU tensor")
+        n, L = input_tiles.shape
+        _validate_common(K, cb, L, sg_size)
+        if tuple(output_tiles_cpu.shape) != (n, L) or tuple(output_indices_cpu.shape) != (n, L):
+            raise RuntimeError("output tensors must have shape (num_tiles, L)")
+        B = temp_costs.size(0)
+        if B < 1 or temp_costs.size(1) != 2 or temp_costs.size(2) != (65536 >> K):
+            raise RuntimeError("temp_costs must have shape (B, 2, 65536 >> K)")
+        search_s = trace_s = 0.0
+        with torch.cuda.device(dev):
+            edges = torch.empty(edges_shape(B, K, L), dtype=torch.uint8, device=f"cuda:{dev}")
+            out_w = torch.empty((n, L), dtype=torch.float32, device=f"cuda:{dev}")
+            out_i = torch.empty((n, L), dtype=torch.int16, device=f"cuda:{dev}")
+            ends = torch.empty(B, dtype=torch.int32, device=f"cuda:{dev}")
+            free = torch.full((B,), -1, dtype=torch.int32, device=f"cuda:{dev}")
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+            for off in range(0, n, B):
+                c = min(B, n - off)
+                x = input_tiles[off:off + c]
+                ev[0].record()
+                self.quantize_tiles_forward_pass(x, temp_costs, edges, free, K, mcg, mul1,
+                                                 L // 2, 0, sg_size)
+                ev[1].record()
+                self.quantize_tiles_backward_pass(temp_costs, edges, out_w[off:off + c],
+                                                  out_i[off:off + c], ends, c, K, mcg, mul1,
+                                                  L // 2, 0, False, sg_size)
+                ev[2].record()
+                self.quantize_tiles_forward_pass(x, temp_costs, edges, ends, K, mcg, mul1, 0, 1,
+                                                 sg_size)
+                ev[3].record()
+                self.quantize_tiles_backward_pass(temp_costs, edges, out_w[off:off + c],
+                                                  out_i[off:off + c], ends, c, K, mcg, mul1, 0, 1,
+                                                  True, sg_size)
+                ev[4].record()
+                ev[4].synchronize()
+                search_s += (ev[0].elapsed_time(ev[1]) + ev[2].elapsed_time(ev[3])) / 1e3
+                trace_s += (ev[1].elapsed_time(ev[2]) + ev[3].elapsed_time(ev[4])) / 1e3
+            output_tiles_cpu.copy_(out_w.cpu())
+            output_indices_cpu.copy_(out_i.cpu())
+        return [search_s, trace_s]
+
     # -------------------------------------------------- device-side helpers
 
     def prepare_tiles(self, raw, out, permute: bool) -> None:

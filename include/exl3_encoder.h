@@ -19,15 +19,21 @@
  *     L = 160 only with MUL1 (quantize_xpu.cpp:93-101).
  *
  * Scratch ("temp_costs" / "temp_edges" in the reference) has a new layout:
- *   temp_costs : fp16 [B][2][E]          terminal path costs of pass 1 / 2,
- *                                         E = 65536 >> K (same as reference)
- *   temp_edges : bytes [B][L + 1][ROWB]  K-bit backpointers per ring row
- *                                         (ROWB = E * BPB / 8) plus a header
- *                                         row per tile.
+ *   temp_costs : fp16 [B][2][E]           terminal path costs of pass 1 / 2,
+ *                                          E = 65536 >> K (same as reference)
+ *   temp_edges : bytes [B][ROWS][ROWB]    per tile, K = 1..7: the fp16 path
+ *                                          costs after every S-th step
+ *                                          (S = 8, 4, 2, 2, 2, 1, 1 for
+ *                                          K = 1..7; ROWB = 2E, group-major),
+ *                                          K = 8: one backpointer byte per
+ *                                          edge and ring row (ROWB = E); plus
+ *                                          a header row.
  * where B is the number of tiles the scratch holds (the reference's batch
- * capacity). exl3_scratch_row_bytes() gives ROWB; BPB is K rounded up to
- * 1, 2, 4 or 8 bits. The reference layout stored int16 predecessor edges,
- * [B][L][E] (quantize_xpu.cpp:153-157).
+ * capacity). exl3_scratch_row_bytes() gives ROWB and
+ * exl3_scratch_edges_bytes(K, L, 1) / ROWB gives ROWS ((L - 2) / S + 2 in
+ * cost-row mode, L + 1 at K = 8). The traceback recomputes the branch of the
+ * path at each step from the stored costs. The reference layout stored int16
+ * predecessor edges, [B][L][E] (quantize_xpu.cpp:153-157).
  */
 #ifndef EXL3_ENCODER_H
 #define EXL3_ENCODER_H
@@ -49,15 +55,17 @@ const char* exl3_version(void);
  * quantize_kernels.sycl:594-601): fp16 bits of all 65536 states. */
 int exl3_decode_codebook(int cb, uint16_t* lut, void* stream);
 
-/* Bytes of one backpointer row (ROWB) for bitrate K. The layout depends on
- * K only, so both kernel variants (and the split passes) share it. */
+/* Bytes of one scratch row (ROWB) for bitrate K. The layout depends on K
+ * only, so both kernel variants (and the split passes) share it. */
 int64_t exl3_scratch_row_bytes(int K);
 
 /* Bytes of temp_edges for `tiles` tiles (replaces the edges term of
  * ScratchEstimator.estimate_scratch, scratch_estimator.py:77-112). */
 int64_t exl3_scratch_edges_bytes(int K, int L, int64_t tiles);
 
-/* Slot of `edge` inside a backpointer row (exposed for host-side checks). */
+/* Position of `edge` inside a scratch row: (h << K) | k for
+ * edge = (k << (16 - 2K)) | h in cost-row mode, edge itself at K = 8
+ * (exposed for host-side checks). */
 int64_t exl3_backpointer_slot(int K, int64_t edge);
 
 /* Replaces quantize_tiles (quantize_xpu.cpp:112-167,
@@ -74,9 +82,10 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
 /* Replaces quantize_tiles_forward_pass (quantize_xpu.cpp:169-215,
  * quantize_kernels.sycl:658-704): one forward add-compare-select pass over
  * the ring with rotation `roll`; tile t is constrained to start from edge
- * pre_states[t] when that is >= 0. Writes all L backpointer rows and the
- * terminal costs to temp_costs[t][cost_slot]. n <= batch capacity.
- * generic = 1 selects the reference-structured kernel. */
+ * pre_states[t] when that is >= 0. Writes every stored cost row (or, at
+ * K = 8, all L backpointer rows), the tile header and the terminal costs to
+ * temp_costs[t][cost_slot]. n <= batch capacity. generic = 1 selects the
+ * reference-structured kernel. */
 int exl3_forward_pass(const float* in, uint16_t* temp_costs, uint8_t* temp_edges,
                       const int32_t* pre_states, int64_t n, int K, int cb, int L, int roll,
                       int cost_slot, int generic, void* stream);

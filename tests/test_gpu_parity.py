@@ -232,6 +232,52 @@ def test_backpointer_rows_k8(ext, torch_mod):
                                       want_costs.view(np.uint16))
 
 
+def test_usm_host_entry_point(ext, torch_mod):
+    """quantize_tiles_usm_host (quantize_xpu.cpp:261-300): CPU output tensors,
+    [search_s, trace_s] timings, chunks of temp_costs' batch size; states and
+    values bit-exact against the C oracle."""
+    rng = np.random.default_rng(4242)
+    raw = rng.normal(0.0, 1.0, size=(5, 256)).astype(np.float16).astype(np.float32)
+    for K in (2, 4):
+        print(f"usm_host K={K}", flush=True)
+        x = torch_mod.from_numpy(raw).cuda()
+        costs = torch_mod.empty((2, 2, 65536 >> K), dtype=torch_mod.float16, device="cuda")
+        out_w = torch_mod.zeros((5, 256), dtype=torch_mod.float32)
+        out_i = torch_mod.zeros((5, 256), dtype=torch_mod.int16)
+        lut = torch_mod.zeros(65536, dtype=torch_mod.float32)
+        t = ext.quantize_tiles_usm_host(x, costs, out_w, out_i, lut, K, False, True)
+        assert len(t) == 2 and all(v >= 0 for v in t)
+        ref = c_oracle.encode_tiles(raw, K=K, cb=2, pre_permute=False)
+        np.testing.assert_array_equal(out_i.numpy().view(np.uint16), ref.output_indices)
+        np.testing.assert_array_equal(out_w.numpy(), ref.reconstructed_perm.astype(np.float32))
+    with pytest.raises(RuntimeError):
+        ext.quantize_tiles_usm_host(x, costs, out_w.cuda(), out_i, lut, 4, False, True)
+
+
+def test_tile_encoder_adapter(torch_mod):
+    """make_xpu_tile_encoder (ldlq.py:344-387): (tiles_n, 256) tensor-core
+    order tiles in, (reconstruction f32, int16 states) out, on the input's
+    device; equal to the C oracle's encode with pre_permute=False."""
+    from exl3_intel_arc_quantizer_amd.tile_encoder import make_xpu_tile_encoder
+    rng = np.random.default_rng(3131)
+    raw = rng.normal(0.0, 0.02, size=(6, 256)).astype(np.float32)
+    raw16 = raw.astype(np.float16).astype(np.float32)
+    enc = make_xpu_tile_encoder(K=4)
+    try:
+        assert enc.K == 4 and enc.cb == 2
+        ref = c_oracle.encode_tiles(raw16, K=4, cb=2, pre_permute=False)
+        # LDLQ hands over unrounded float32 tiles; the encoder rounds to fp16
+        # first (xpu_quantizer.py:654-655), as the oracle's raw16 does.
+        for tiles in (torch_mod.from_numpy(raw).cuda(), torch_mod.from_numpy(raw)):
+            recon, idx = enc(tiles)
+            assert recon.device == tiles.device and idx.dtype == torch_mod.int16
+            np.testing.assert_array_equal(idx.cpu().numpy().view(np.uint16), ref.output_indices)
+            np.testing.assert_array_equal(recon.cpu().numpy(),
+                                          ref.reconstructed_perm.astype(np.float32))
+    finally:
+        enc.encoder.arena.release()
+
+
 def test_traceback_modes_and_variants_agree():
     """tests/test_xpu_quantizer.py:299-330."""
     rng = np.random.default_rng(909)
