@@ -156,6 +156,31 @@ def forward_kernel_roofline(batch, torch, reps=3):
                             "(copy-kernel calibration), profiles/forward_pass_pmc_config2.md"}
 
 
+def _numpy_encode_one(args):
+    tile, K = args
+    from oracle.reference_encoder import ReferenceTrellisEncoder
+    ReferenceTrellisEncoder(K=K, cb=2).encode_tile(tile, pre_permute=True)
+    return 0
+
+
+def cpu_baseline_numpy(tiles, K, cores):
+    """The numpy restatement of the reference encoder (oracle/reference_encoder.py,
+    op for op the reference's reference_encoder.py), one tile per task on a
+    pool of `cores` processes, on a bounded sample of the same workload. Run
+    before the GPU is initialised (the pool forks)."""
+    import multiprocessing as mp
+    n = 4 * cores
+    ctx = mp.get_context("fork")
+    with ctx.Pool(cores) as pool:
+        pool.map(_numpy_encode_one, [(tiles[0], K)] * cores)       # imports, warm
+        t0 = time.perf_counter()
+        pool.map(_numpy_encode_one, [(tiles[i], K) for i in range(n)], chunksize=1)
+        dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 3), "unit": "tiles/s", "cores": cores, "kind": "port",
+            "sample": f"first {n} tiles of the benchmark matrix at K={K} ({dt:.1f} s, numpy "
+                      "restatement of reference_encoder.py, one process per core)"}
+
+
 def cpu_baseline(tiles, K):
     """The C oracle (oracle/libexl3_oracle.so, a port of the reference's CPU
     encoder) on a bounded sample of the same workload, all host cores."""
@@ -194,11 +219,21 @@ def main() -> int:
               "once)", file=sys.stderr)
         return 2
 
+    tiles = config2_tiles()
+    k_list = [int(k) for k in args.k_list.split(",")]
+    head = k_list[0]
+    cpu = cpu_np = None
+    if not args.no_cpu_baseline and not args.profile_forward:
+        # Host baselines first: nothing has touched the GPU yet.
+        cpu = cpu_baseline(tiles, head)
+        cpu_np = cpu_baseline_numpy(tiles, head, cpu["cores"])
+        print(f"# CPU baselines at K={head}: C {cpu['value']} tiles/s, numpy {cpu_np['value']} "
+              f"tiles/s on {cpu['cores']} cores", file=sys.stderr, flush=True)
+
     import torch
 
     from exl3_intel_arc_quantizer_amd.gpu_quantizer import build_quantize_extension
     ext = build_quantize_extension()
-    tiles = config2_tiles()
 
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
@@ -210,7 +245,6 @@ def main() -> int:
         del src, dst
         torch.cuda.empty_cache()
 
-    k_list = [int(k) for k in args.k_list.split(",")]
     if args.profile_forward:
         for K in k_list:
             b = DeviceBatch(tiles, K, torch, ext)
@@ -250,8 +284,6 @@ def main() -> int:
             del b
             torch.cuda.empty_cache()
 
-    head = k_list[0]
-    cpu = None if args.no_cpu_baseline else cpu_baseline(tiles, head)
     main_k = results[head]
     line = {
         "metric": METRIC,
@@ -271,6 +303,7 @@ def main() -> int:
                    "tiles": 4096, "K": head, "codebook": "mul1"},
         "roofline": main_k["roofline"],
         "cpu_baseline": cpu,
+        "cpu_baseline_numpy": cpu_np,
     }
     for K in k_list[1:]:
         line[f"k{K}"] = {"value": round(results[K]["tiles_per_s"], 1), "unit": "tiles/s",

@@ -579,8 +579,32 @@ __device__ __forceinline__ uint32_t row_pos(uint32_t x) {
   return ((x & ((1u << KS) - 1u)) << K) | (x >> KS);
 }
 
+// Leaves of a depth-D tree into LDS: leaf n = (k_0 .. k_D) is C_{r0} at
+// x_D(n), read from the stored row as aligned vectors of sibling costs.
+template <int K, int D>
+__device__ __forceinline__ void tb_load(const uint16_t* __restrict__ row, uint32_t edge,
+                                        uint16_t* leaf, int lane) {
+  constexpr int NB = 1 << K, KS = 16 - 2 * K;
+  constexpr int NLOG = K * (D + 1);
+  constexpr int RLOG = NLOG > 6 ? NLOG - 6 : 0;
+  constexpr int R = 1 << RLOG;
+  constexpr int CH = R < NB ? R : NB;
+  constexpr int NLEAF = 1 << NLOG;
+  const uint32_t h0 = edge >> K;
+  if (((uint32_t)lane << RLOG) >= (uint32_t)NLEAF) return;
+#pragma unroll
+  for (int c = 0; c < R / CH; ++c) {
+    const uint32_t n = ((uint32_t)lane << RLOG) | (uint32_t)(c * CH);
+    uint32_t x = ((n >> (K * D)) << KS) | h0;
+#pragma unroll
+    for (int m = 1; m <= D; ++m) x = (((n >> (K * (D - m))) & (NB - 1)) << KS) | (x >> K);
+    typedef typename U16Vec<CH>::type vec;
+    *reinterpret_cast<vec*>(leaf + n) = *reinterpret_cast<const vec*>(row + row_pos<K>(x));
+  }
+}
+
 template <int K, int CB, int D, bool INIT>
-__device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ row, uint32_t edge,
+__device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ leaf, uint32_t edge,
                                               const uint16_t* __restrict__ wbits, int ri, int L,
                                               int lane, int pre) {
   constexpr int NB = 1 << K, KR = 16 - K, KS = 16 - 2 * K;
@@ -613,7 +637,7 @@ __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ row, 
 #pragma unroll
     for (int c = 0; c < R / CH; ++c) {
       const typename U16Vec<CH>::type q =
-          *reinterpret_cast<const typename U16Vec<CH>::type*>(row + row_pos<K>(xs[c * CH][D]));
+          *reinterpret_cast<const typename U16Vec<CH>::type*>(leaf + nid[c * CH]);
 #pragma unroll
       for (int u = 0; u < CH; ++u) v[c * CH + u] = q[u];
     }
@@ -668,21 +692,37 @@ __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ row, 
   return key & 0xFFFFu;
 }
 
-// tb_branch for the runtime distance d in [D, row_stride(K)).
+// tb_branch / tb_load for the runtime distance d in [D, row_stride(K)).
 template <int K, int CB, int D>
-__device__ __forceinline__ uint32_t tb_dispatch(int d, const uint16_t* __restrict__ row,
-                                                uint32_t edge, const uint16_t* __restrict__ wbits,
-                                                int ri, int L, int lane, int pre) {
+__device__ __forceinline__ uint32_t tb_dispatch(int d, const uint16_t* leaf, uint32_t edge,
+                                                const uint16_t* __restrict__ wbits, int ri, int L,
+                                                int lane, int pre) {
   if constexpr (D + 1 < exl3::row_stride(K)) {
-    if (d != D) return tb_dispatch<K, CB, D + 1>(d, row, edge, wbits, ri, L, lane, pre);
+    if (d != D) return tb_dispatch<K, CB, D + 1>(d, leaf, edge, wbits, ri, L, lane, pre);
   }
-  return tb_branch<K, CB, D, false>(row, edge, wbits, ri, L, lane, pre);
+  return tb_branch<K, CB, D, false>(leaf, edge, wbits, ri, L, lane, pre);
 }
 
+template <int K, int D>
+__device__ __forceinline__ void tb_load_dispatch(int d, const uint16_t* __restrict__ row,
+                                                 uint32_t edge, uint16_t* leaf, int lane) {
+  if constexpr (D + 1 < exl3::row_stride(K)) {
+    if (d != D) return tb_load_dispatch<K, D + 1>(d, row, edge, leaf, lane);
+  }
+  tb_load<K, D>(row, edge, leaf, lane);
+}
+
+// The tree of step i-1 is the subtree of step i's tree under the branch
+// step i chose, so one load of a stored row's tree (at the first step that
+// needs it) serves every step down to that row: the next step's leaves start
+// at base + k * NB^d in LDS. One dependent HBM load per stride of steps.
 template <int K, int CB>
 __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
   constexpr int KR = 16 - K;
   constexpr int STRIDE = exl3::row_stride(K);
+  constexpr int MAXLEAF = 1 << (K * STRIDE);
+  __shared__ __attribute__((aligned(16))) uint16_t s_leaf[MAXLEAF];
+  __shared__ uint16_t s_wbits[256];  // the tile's fp16 inputs, ring order
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   const int L = a.L;
@@ -690,8 +730,13 @@ __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
   const uint8_t* hdr = blk + a.hdr_offset;
   const int row_bytes = a.lay.row_bytes;
   const int pre = reinterpret_cast<const int32_t*>(hdr)[exl3::HDR_PRE_STATE];
-  const uint16_t* wbits = reinterpret_cast<const uint16_t*>(hdr + exl3::HDR_W_BYTES);
+  const uint16_t* wsrc = reinterpret_cast<const uint16_t*>(hdr + exl3::HDR_W_BYTES);
+  for (int r = lane; r < L; r += 64) s_wbits[r] = wsrc[r];
+  __syncthreads();
+  const uint16_t* wbits = s_wbits;
   uint32_t edge = (uint32_t)a.start[(int64_t)t * a.start_stride] & ((65536u >> K) - 1u);
+  int loaded = -1;  // stored row whose tree is in s_leaf
+  int base = 0;     // offset of the current step's leaves
 
   for (int i = L - 1; i >= 0; --i) {
     int ri = i + a.roll;
@@ -701,9 +746,18 @@ __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
       k = tb_branch<K, CB, 0, true>(nullptr, edge, wbits, ri, L, lane, pre);
     } else {
       const int d = (i - 1) % STRIDE;
-      const uint16_t* row = reinterpret_cast<const uint16_t*>(
-          blk + (int64_t)((i - 1 - d) / STRIDE) * row_bytes);
-      k = tb_dispatch<K, CB, 0>(d, row, edge, wbits, ri, L, lane, pre);
+      const int r0 = i - 1 - d;
+      if (r0 != loaded) {
+        const uint16_t* row = reinterpret_cast<const uint16_t*>(
+            blk + (int64_t)(r0 / STRIDE) * row_bytes);
+        __syncthreads();  // the previous tree's last readers are done
+        tb_load_dispatch<K, 0>(d, row, edge, s_leaf, lane);
+        __syncthreads();
+        loaded = r0;
+        base = 0;
+      }
+      k = tb_dispatch<K, CB, 0>(d, s_leaf + base, edge, wbits, ri, L, lane, pre);
+      base += (int)k << (K * d);
     }
     const uint32_t sigma = (k << KR) | edge;
     if (a.write && lane == 0) {
