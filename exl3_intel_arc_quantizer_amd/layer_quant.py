@@ -1,0 +1,270 @@
+"""Linear-layer and decoder-layer quantisation driver on the GPU
+(reference: exl3_quant/layer_quant.py, calibration.py:242-407).
+
+``quantize_linear_module`` runs one projection through the EXL3 pipeline:
+regularise the weight (scales, blockwise Hadamard), rotate the Hessian with
+the same transforms, factor it (``block_ldl``), quantise with LDLQ error
+feedback through the HIP tile encoder, map the reconstruction back to the
+original basis and report the distortion and Hessian proxy metrics.
+``quantize_decoder_layer`` does every bias-free ``nn.Linear`` of a layer
+with one shared encoder and scratch arena. Everything stays on the GPU; the
+encoder is the only consumer of the trellis kernels and there is no CPU
+fallback.
+
+``hessian_from_activations`` and ``hessian_groups`` restate the reference's
+calibration: H = X^T X / tokens in float32, plus lambda * mean(diag H) on
+the diagonal and a floor on inactive channels; projections that read the
+same input share one Hessian.
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+from .hadamard import HAD_DIM, blockwise_preapply_had_l_, blockwise_preapply_had_r_, \
+    weight_from_quantized
+from .ldlq import DEFAULT_BLOCK_SIZE, DEFAULT_BUF_SIZE_K, BlockLDLResult, block_ldl, ldlq
+from .regularize import RegularizeResult, regularize
+from .tile_encoder import TileEncoder, make_xpu_tile_encoder
+from .trellis_format import CB_MUL1
+
+DEFAULT_DAMPING_LAMBDA = 0.01        # calibration.py:43
+DEFAULT_ZERO_CHANNEL_FLOOR = 1e-7    # calibration.py:44
+
+
+# ------------------------------------------------------------------ Hessians
+
+def hessian_from_activations(x: torch.Tensor, damping_lambda: float = DEFAULT_DAMPING_LAMBDA,
+                             zero_floor: float = DEFAULT_ZERO_CHANNEL_FLOOR,
+                             chunk_tokens: int = 8192) -> Tuple[torch.Tensor, float]:
+    """Hessian of one projection input: sum over token chunks of X^T X in
+    float32 (calibration.py:337-352), divided by the token count, diagonal
+    damped by lambda * mean(diag) and floored at ``zero_floor``
+    (calibration.py:359-385). Returns (H, applied damping)."""
+    d = x.shape[-1]
+    flat = x.reshape(-1, d)
+    H = torch.zeros((d, d), dtype=torch.float32, device=x.device)
+    for s in range(0, flat.shape[0], chunk_tokens):
+        xf = flat[s:s + chunk_tokens].to(torch.float32)
+        H += xf.T @ xf
+    H /= max(1, flat.shape[0])
+    diag = H.diagonal()
+    damp = max(1e-8, damping_lambda * diag.mean().item())
+    diag.add_(damp)
+    floor = torch.as_tensor(zero_floor, dtype=diag.dtype, device=diag.device)
+    diag.copy_(torch.where(diag.abs() < zero_floor, floor, diag))
+    return H, damp
+
+
+def hessian_groups(module_names: List[str]) -> Dict[str, List[str]]:
+    """Projections that read the same input share one Hessian
+    (calibration.py:242-289): q/k/v, the GatedDeltaNet input projections,
+    gate/up; every other projection is its own group."""
+    groups: Dict[str, List[str]] = {}
+    for key, members in (("self_attn.input", ("self_attn.q_proj", "self_attn.k_proj",
+                                              "self_attn.v_proj")),
+                         ("self_attn.o_proj", ("self_attn.o_proj",)),
+                         ("linear_attn.input", ("linear_attn.in_proj_qkv",
+                                                "linear_attn.in_proj_z",
+                                                "linear_attn.in_proj_b",
+                                                "linear_attn.in_proj_a")),
+                         ("linear_attn.out_proj", ("linear_attn.out_proj",)),
+                         ("mlp.input", ("mlp.gate_proj", "mlp.up_proj")),
+                         ("mlp.down_proj", ("mlp.down_proj",))):
+        present = [m for m in members if m in module_names]
+        if present:
+            groups[key] = present
+    assigned = {m for ms in groups.values() for m in ms}
+    for name in module_names:
+        if name not in assigned:
+            groups[name] = [name]
+    return groups
+
+
+# ------------------------------------------------------------------- results
+
+@dataclass
+class ModuleMetrics:
+    """Distortion and proxy metrics of one quantised projection (layer_quant.py:49-60)."""
+
+    mse: float
+    relative_frobenius_error: float
+    tile_distortion: float
+    proxy_loss: float
+    normalized_proxy_loss: float
+    factorization_residual: float
+    retries: int
+    g_scale: float
+    elapsed_seconds: float
+    encoder_seconds: float = 0.0
+    encoder_calls: int = 0
+
+
+@dataclass
+class QuantizedModuleResult:
+    """Outputs of a quantised projection (layer_quant.py:63-77)."""
+
+    name: str
+    K: int
+    cb: int
+    original_shape: Tuple[int, int]
+    weight_orig: torch.Tensor
+    w_hat: torch.Tensor
+    encoded: torch.Tensor
+    su: torch.Tensor
+    sv: torch.Tensor
+    metrics: ModuleMetrics
+    regularize_result: RegularizeResult
+    ldl_result: BlockLDLResult
+
+
+@dataclass
+class LayerQuantizationReport:
+    """Report of a decoder-layer conversion (layer_quant.py:80-92)."""
+
+    K: int
+    codebook: str
+    total_elapsed_seconds: float
+    module_results: Dict[str, QuantizedModuleResult]
+    total_proxy_loss: float
+    mean_mse: float
+    peak_device_memory_bytes: int
+    scratch_arena_reused: bool
+    device_index: int
+    tiles: int = 0
+    encoder_seconds: float = 0.0
+    extra: dict = field(default_factory=dict)
+
+
+def compute_factorization_residual(H: torch.Tensor, chol: torch.Tensor) -> float:
+    """||H - L L^T||_F / ||H||_F (layer_quant.py:95-101)."""
+    diff = H - chol @ chol.T
+    return float(torch.linalg.norm(diff).item() / max(1e-12, torch.linalg.norm(H).item()))
+
+
+def compute_proxy_loss(W: torch.Tensor, W_hat: torch.Tensor,
+                       H: torch.Tensor) -> Tuple[float, float]:
+    """tr(E^T H E) as sum((H E) * E), E = W - W_hat, and its ratio to
+    tr(W^T H W) (layer_quant.py:104-127)."""
+    E = (W - W_hat).to(dtype=torch.float32, device=H.device)
+    H32 = H.to(torch.float32)
+    proxy = float(((H32 @ E) * E).sum().item())
+    W32 = W.to(dtype=torch.float32, device=H.device)
+    energy = max(1e-12, float(((H32 @ W32) * W32).sum().item()))
+    return proxy, proxy / energy
+
+
+# -------------------------------------------------------------------- driver
+
+def quantize_linear_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int = 2,
+                           cb: int = CB_MUL1, tile_encoder: Optional[TileEncoder] = None,
+                           skip_g_scale: bool = True, buf_size_k: int = DEFAULT_BUF_SIZE_K,
+                           block_size: int = DEFAULT_BLOCK_SIZE) -> QuantizedModuleResult:
+    """Quantise one linear weight with LDLQ (layer_quant.py:130-265). The
+    weight is (out, in) as in ``nn.Linear`` or already (in, out) = (k, n);
+    ``H`` is (in, in). Runs on the device of ``H``, which must be a GPU."""
+    t0 = time.time()
+    if weight.dim() != 2:
+        raise ValueError(f"weight must be 2D, got shape {tuple(weight.shape)}")
+    device = H.device
+    if device.type != "cuda":
+        raise ValueError("quantize_linear_module runs on the GPU; move H to a cuda device")
+    k_dim = H.shape[0]
+    if weight.shape[1] == k_dim:
+        W = weight.T.to(device=device, dtype=torch.float32).contiguous()
+    elif weight.shape[0] == k_dim:
+        W = weight.to(device=device, dtype=torch.float32).clone()
+    else:
+        raise ValueError(f"Weight shape {tuple(weight.shape)} does not match Hessian dim {k_dim}")
+    k, n = W.shape
+    if tile_encoder is None:
+        tile_encoder = make_xpu_tile_encoder(K=K, device_index=device.index or 0)
+    enc_k = getattr(tile_encoder, "K", None)
+    if enc_k is not None and enc_k != K:
+        raise ValueError(f"Tile encoder K={enc_k} does not match the requested K={K}.")
+    if not skip_g_scale:
+        raise ValueError("the global-scale search (skip_g_scale=False) is not part of this build")
+
+    su = torch.ones((k, 1), dtype=torch.float32, device=device)
+    sv = torch.ones((1, n), dtype=torch.float32, device=device)
+    reg = regularize(weight=W, su=su, sv=sv, H_diag=H.diagonal(), skip_g_scale=True,
+                     had_dim=HAD_DIM)
+
+    H_work = H.to(torch.float32).clone()
+    blockwise_preapply_had_l_(H_work, HAD_DIM)
+    blockwise_preapply_had_r_(H_work, HAD_DIM)
+    ldl = block_ldl(H_work, block_size=block_size)
+    fact_residual = compute_factorization_residual(H_work, ldl.cholesky)
+
+    sync = (lambda: torch.cuda.synchronize(device)) if device.type == "cuda" else None
+    lq = ldlq(weight=reg.weight, L=ldl.transformed, encode_tiles=tile_encoder,
+              buf_size_k=buf_size_k, synchronize=sync)
+    w_hat = weight_from_quantized(lq.weight_q, reg.su, reg.sv)
+
+    diff = W - w_hat
+    proxy, norm_proxy = compute_proxy_loss(W, w_hat, H)
+    metrics = ModuleMetrics(
+        mse=float(diff.pow(2).mean().item()),
+        relative_frobenius_error=float(torch.linalg.norm(diff).item()
+                                       / max(1e-12, torch.linalg.norm(W).item())),
+        tile_distortion=float((reg.weight - lq.weight_q).pow(2).mean().item()),
+        proxy_loss=proxy, normalized_proxy_loss=norm_proxy,
+        factorization_residual=fact_residual, retries=ldl.retries, g_scale=reg.g_scale,
+        elapsed_seconds=time.time() - t0, encoder_seconds=lq.encoder_seconds,
+        encoder_calls=lq.encoder_calls)
+    return QuantizedModuleResult(name=name, K=K, cb=cb, original_shape=(k, n), weight_orig=W,
+                                 w_hat=w_hat, encoded=lq.encoded, su=reg.su, sv=reg.sv,
+                                 metrics=metrics, regularize_result=reg, ldl_result=ldl)
+
+
+def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Tensor], K: int = 2,
+                           cb: int = CB_MUL1, device: Optional[torch.device] = None,
+                           skip_g_scale: bool = True, buf_size_k: int = DEFAULT_BUF_SIZE_K,
+                           block_size: int = DEFAULT_BLOCK_SIZE, memory_policy=None,
+                           module_names: Optional[List[str]] = None) -> LayerQuantizationReport:
+    """Quantise every bias-free ``nn.Linear`` of a decoder layer (or the
+    ``module_names`` subset) with one shared encoder and scratch arena
+    (layer_quant.py:268-387)."""
+    from .gpu_quantizer import ScratchArena
+    from .memory_policy import MemoryPolicy
+
+    t_start = time.time()
+    if device is None:
+        device = torch.device("cuda:0")
+    if device.type != "cuda":
+        raise ValueError("quantize_decoder_layer runs on the GPU")
+    policy = memory_policy or MemoryPolicy()
+    arena = ScratchArena(device_index=device.index or 0, policy=policy)
+    encoder = make_xpu_tile_encoder(K=K, device_index=device.index or 0, arena=arena)
+    available = {name: m for name, m in layer.named_modules()
+                 if isinstance(m, torch.nn.Linear) and m.bias is None}
+    selected = list(available) if module_names is None else list(module_names)
+    missing = [n for n in selected if n not in available]
+    if missing:
+        raise KeyError(f"requested modules are not bias-free nn.Linear submodules: {missing}")
+    torch.cuda.reset_peak_memory_stats(device)
+    results: Dict[str, QuantizedModuleResult] = {}
+    try:
+        for name in selected:
+            if name not in hessians:
+                raise KeyError(f"Hessian missing for module {name}")
+            results[name] = quantize_linear_module(
+                name=name, weight=available[name].weight.data, H=hessians[name].to(device),
+                K=K, cb=cb, tile_encoder=encoder, skip_g_scale=skip_g_scale,
+                buf_size_k=buf_size_k, block_size=block_size)
+            torch.cuda.synchronize(device)
+    finally:
+        arena.release()
+    tiles = sum(r.original_shape[0] * r.original_shape[1] // 256 for r in results.values())
+    return LayerQuantizationReport(
+        K=K, codebook="mul1" if cb == CB_MUL1 else str(cb),
+        total_elapsed_seconds=time.time() - t_start, module_results=results,
+        total_proxy_loss=sum(r.metrics.proxy_loss for r in results.values()),
+        mean_mse=float(sum(r.metrics.mse for r in results.values()) / max(1, len(results))),
+        peak_device_memory_bytes=int(torch.cuda.max_memory_allocated(device)),
+        scratch_arena_reused=True, device_index=device.index or 0, tiles=tiles,
+        encoder_seconds=sum(r.metrics.encoder_seconds for r in results.values()))
