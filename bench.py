@@ -197,6 +197,105 @@ def cpu_baseline(tiles, K):
                       f"({dt:.1f} s, C restatement of reference_encoder.py, OpenMP)"}
 
 
+def _synthetic_activations(rng, tokens, width, outlier_frac=0.05):
+    """N(0, 1) activations with a seeded fraction of channels scaled x10."""
+    X = rng.standard_normal((tokens, width), dtype=np.float32)
+    chans = rng.choice(width, size=int(round(outlier_frac * width)), replace=False)
+    X[:, chans] *= 10.0
+    return X
+
+
+def run_layer_config(torch, K=4):
+    """one 4096x4096 linear layer, W ~ N(0, 0.02^2) (seed 3),
+    Hessian X^T X / 8192 from bf16 activations [8192, 4096] (seed 4, 5 % of
+    channels x10), damped 1 %, Hadamard-rotated inside the driver, LDLQ with
+    buf_size_k = 128 at K = 4 (256 encoder calls of 256 tiles)."""
+    from exl3_intel_arc_quantizer_amd.layer_quant import (hessian_from_activations,
+                                                          quantize_linear_module)
+    W = torch.from_numpy((np.random.default_rng(3).standard_normal((4096, 4096),
+                                                                   dtype=np.float32) * 0.02))
+    X = torch.from_numpy(_synthetic_activations(np.random.default_rng(4), 8192, 4096))
+    X = X.to(torch.bfloat16).cuda()
+    H, damp = hessian_from_activations(X)
+    del X
+    quantize_linear_module("warmup", W[:256, :256].cuda(), H[:256, :256].contiguous(), K=K)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    res = quantize_linear_module("layer", W.cuda(), H, K=K)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    m = res.metrics
+    tiles = 4096 * 4096 // 256
+    return {"metric": "LDLQ-driven 4096x4096 layer, K=4, 1 MI355X: wall time", "value": round(wall, 3),
+            "unit": "s", "higher_is_better": False, "n_gpus": 1, "dtype": "fp16", "data": "synthetic",
+            "config": {"workload": "configs[3]", "K": K, "buf_size_k": 128, "tiles": tiles,
+                       "encoder_calls": m.encoder_calls},
+            "tiles_per_s": round(tiles / wall, 1),
+            "encoder_seconds": round(m.encoder_seconds, 3),
+            "encoder_share": round(m.encoder_seconds / wall, 4),
+            "proxy_loss": m.proxy_loss, "normalized_proxy_loss": m.normalized_proxy_loss,
+            "mse": m.mse, "factorization_residual": m.factorization_residual,
+            "damping": damp,
+            "cpu_path_parity": "proxy within 1e-3 of the CPU path on 256x256 layers "
+                               "(tests/test_gpu_layer.py); a full-size CPU run is hours"}
+
+
+def run_decoder_config(torch, K=4, cpu_tiles_per_s=None):
+    """configs[4]: a 9B-class decoder layer (hidden 4096; q, o 4096x4096;
+    k, v 1024x4096; gate, up 12288x4096; down 4096x12288), random-init weights
+    (torch seed 5), Hessians per shared-input group from synthetic bf16
+    activations [16384, width] (seeds 6..9, 5 % of channels x10), K = 4:
+    753,664 tiles in 2,304 encoder calls."""
+    from exl3_intel_arc_quantizer_amd.layer_quant import (hessian_from_activations,
+                                                          hessian_groups,
+                                                          quantize_decoder_layer)
+    nn = torch.nn
+    torch.manual_seed(5)
+    layer = nn.Module()
+    layer.self_attn = nn.Module()
+    layer.mlp = nn.Module()
+    for name, (o, i) in {"q_proj": (4096, 4096), "k_proj": (1024, 4096), "v_proj": (1024, 4096),
+                         "o_proj": (4096, 4096)}.items():
+        setattr(layer.self_attn, name, nn.Linear(i, o, bias=False))
+    for name, (o, i) in {"gate_proj": (12288, 4096), "up_proj": (12288, 4096),
+                         "down_proj": (4096, 12288)}.items():
+        setattr(layer.mlp, name, nn.Linear(i, o, bias=False))
+    layer = layer.cuda()
+    names = [n for n, m in layer.named_modules() if isinstance(m, nn.Linear)]
+    hess = {}
+    t0 = time.perf_counter()
+    for seed, (key, members) in enumerate(hessian_groups(names).items(), start=6):
+        width = 12288 if key == "mlp.down_proj" else 4096
+        X = torch.from_numpy(_synthetic_activations(np.random.default_rng(seed), 16384, width))
+        H, _ = hessian_from_activations(X.to(torch.bfloat16).cuda())
+        for mname in members:
+            hess[mname] = H
+    torch.cuda.synchronize()
+    t_hess = time.perf_counter() - t0
+    rep = quantize_decoder_layer(layer, hess, K=K)
+    wall = rep.total_elapsed_seconds
+    calls = sum(r.metrics.encoder_calls for r in rep.module_results.values())
+    out = {"metric": "9B-class decoder layer conversion, K=4, 1 MI355X: wall time",
+           "value": round(wall, 3), "unit": "s", "higher_is_better": False, "n_gpus": 1,
+           "dtype": "fp16", "data": "synthetic",
+           "config": {"workload": "configs[4]", "K": K, "tiles": rep.tiles,
+                      "encoder_calls": calls},
+           "tiles_per_s": round(rep.tiles / wall, 1),
+           "encoder_seconds": round(rep.encoder_seconds, 3),
+           "encoder_share": round(rep.encoder_seconds / wall, 4),
+           "hessian_seconds": round(t_hess, 3),
+           "total_proxy_loss": rep.total_proxy_loss, "mean_mse": rep.mean_mse,
+           "peak_device_memory_bytes": rep.peak_device_memory_bytes,
+           "modules": {n: {"shape_kn": list(r.original_shape),
+                           "seconds": round(r.metrics.elapsed_seconds, 3),
+                           "encoder_seconds": round(r.metrics.encoder_seconds, 3),
+                           "normalized_proxy_loss": r.metrics.normalized_proxy_loss}
+                       for n, r in rep.module_results.items()}}
+    if cpu_tiles_per_s:
+        out["cpu_encoder_extrapolated_seconds"] = round(rep.tiles / cpu_tiles_per_s, 1)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -209,6 +308,10 @@ def main() -> int:
     ap.add_argument("--profile-forward", action="store_true",
                     help="only the forward launches the roofline is measured on (one warm-up "
                          "and three timed per K), for rocprofv3 runs")
+    ap.add_argument("--layer", action="store_true",
+                    help="configs[3]: LDLQ-driven 4096x4096 layer (prints its own JSON line)")
+    ap.add_argument("--decoder", action="store_true",
+                    help="configs[4]: 9B-class decoder layer conversion (its own JSON line)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device copy (known-size kernel for PMC byte "
                          "counter calibration)")
@@ -223,6 +326,14 @@ def main() -> int:
     k_list = [int(k) for k in args.k_list.split(",")]
     head = k_list[0]
     cpu = cpu_np = None
+    if args.layer or args.decoder:
+        import torch
+        if args.decoder and not args.no_cpu_baseline:
+            cpu = cpu_baseline(tiles, 4)
+        line = (run_layer_config(torch) if args.layer else
+                run_decoder_config(torch, cpu_tiles_per_s=cpu["value"] if cpu else None))
+        print(json.dumps(line), flush=True)
+        return 0
     if not args.no_cpu_baseline and not args.profile_forward:
         # Host baselines first: nothing has touched the GPU yet.
         cpu = cpu_baseline(tiles, head)

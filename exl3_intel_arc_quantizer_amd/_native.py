@@ -37,7 +37,7 @@ _SIGNATURES = {
                                    _c_int, _c_int, _c_int, _c_vp]),
     "exl3_backward_pass": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_int,
                                     _c_int, _c_int, _c_int, _c_int, _c_vp]),
-    "exl3_prepare_tiles": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
+    "exl3_prepare_tiles": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp, _c_vp]),
     "exl3_finalize_tiles": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                      _c_i64, _c_int, _c_int, _c_int, _c_vp]),
     "exl3_pack_trellis": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
@@ -341,16 +341,25 @@ class QuantizeExtension:
 
     # -------------------------------------------------- device-side helpers
 
-    def prepare_tiles(self, raw, out, permute: bool) -> None:
+    def prepare_tiles(self, raw, out, permute: bool, nan_count=None) -> None:
+        """fp16-round (and optionally permute) ``raw`` into ``out``; a given
+        ``nan_count`` (device int32, one element) gains one per NaN value."""
         torch = _torch()
         dev = _check_device_tensor(raw, "raw", torch.float32, 2)
         _check_device_tensor(out, "out", torch.float32, 2)
         n, L = raw.shape
         if tuple(out.shape) != (n, L):
             raise RuntimeError("out must match raw")
+        counter = None
+        if nan_count is not None:
+            if (not isinstance(nan_count, torch.Tensor) or nan_count.dtype != torch.int32
+                    or nan_count.device != raw.device or nan_count.numel() < 1):
+                raise RuntimeError("nan_count must be an int32 tensor on the tiles' device")
+            counter = nan_count.data_ptr()
         with torch.cuda.device(dev):
             _check(self.lib.exl3_prepare_tiles(raw.data_ptr(), out.data_ptr(), n, L,
-                                               int(bool(permute)), _stream(dev)), "prepare_tiles")
+                                               int(bool(permute)), counter, _stream(dev)),
+                   "prepare_tiles")
 
     def finalize_tiles(self, x, raw, out_w, out_idx, packed, path_cost, distortion, recon_orig,
                        K: int, permuted: bool) -> None:

@@ -772,13 +772,16 @@ __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
 
 // ---------------------------------------------------------- prepare/finalize
 
+// nan_count (may be NULL) gains one per NaN input value, so a caller can
+// reject NaN tiles without a device-to-host round trip per batch.
 __global__ void prepare_kernel(const float* __restrict__ raw, float* __restrict__ out, int64_t n,
-                               int L, int permute) {
+                               int L, int permute, int32_t* __restrict__ nan_count) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= n * L) return;
   const int64_t t = idx / L;
   const int i = (int)(idx - t * L);
   const float v = raw[t * L + (permute ? tc_perm(i) : i)];
+  if (nan_count != nullptr && v != v) atomicAdd(nan_count, 1);
   out[idx] = (float)(f16)v;
 }
 
@@ -1145,13 +1148,13 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
 }
 
 int exl3_prepare_tiles(const float* raw, float* out, int64_t n, int L, int permute,
-                       void* stream) {
+                       int32_t* nan_count, void* stream) {
   if (n <= 0 || L <= 0) return set_error("bad tile batch shape");
   if (permute && L != 256) return set_error("pre_permute=True is only defined for L=256");
   const int64_t total = n * L;
   const int block = 256;
   hipLaunchKernelGGL(prepare_kernel, dim3((unsigned)((total + block - 1) / block)), dim3(block), 0,
-                     as_stream(stream), raw, out, n, L, permute);
+                     as_stream(stream), raw, out, n, L, permute, nan_count);
   return check_launch("prepare_tiles");
 }
 

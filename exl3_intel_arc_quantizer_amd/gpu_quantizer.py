@@ -207,8 +207,12 @@ class ScratchArena:
 
     def acquire(self, k: int, tile_len: int = 256, requested_b: Optional[int] = None,
                 distinct_staging_bytes: int = 0,
-                allocator_hook: Optional[Callable[[int], None]] = None):
-        """Return ``(temp_costs, temp_edges, admitted_b)`` (xpu_quantizer.py:313-506)."""
+                allocator_hook: Optional[Callable[[int], None]] = None,
+                synchronize_reuse: bool = True):
+        """Return ``(temp_costs, temp_edges, admitted_b)`` (xpu_quantizer.py:313-506).
+        ``synchronize_reuse=False`` hands a resident buffer back without the
+        device synchronisation: correct when every user of the buffers
+        launches on one HIP stream, whose order already serialises them."""
         import torch
 
         target_b = requested_b if requested_b is not None else self.default_cap_b
@@ -218,7 +222,8 @@ class ScratchArena:
         if (self._key is not None and self._key[0] == self.device_index and self._key[1] == k
                 and self._key[2] == tile_len and self._key[3] >= target_b
                 and self._temp_costs is not None and self._temp_edges is not None):
-            torch.cuda.synchronize(self.device_index)
+            if synchronize_reuse:
+                torch.cuda.synchronize(self.device_index)
             self.reuses += 1
             snap = capture_snapshot(self.device_index)
             out_bytes = int(torch.cuda.memory_allocated(self.device_index))
@@ -413,7 +418,7 @@ class XPUTrellisEncoder:
             raise ValueError(f"Unknown traceback_mode {mode!r}")
 
     def _run_chunks(self, ext, x_dev, out_w, out_i, temp_costs, temp_edges, admitted_b, mode,
-                    timings):
+                    timings, synchronize=True):
         """Encode x_dev (n, L) kernel-order tiles chunk by chunk."""
         import torch
 
@@ -425,8 +430,9 @@ class XPUTrellisEncoder:
             ext.quantize_tiles(x_dev, out_w, out_i, temp_costs[:admitted_b],
                                temp_edges[:admitted_b], self.K, self.mcg_flag, self.mul1_flag,
                                self.sg_size, self.force_global_costs, self.wave_cap_override)
-            torch.cuda.synchronize(self.device_index)
-            timings["search"] += time.perf_counter() - ts
+            if synchronize:
+                torch.cuda.synchronize(self.device_index)
+                timings["search"] += time.perf_counter() - ts
             return -(-n // admitted_b)
         pre = torch.full((admitted_b,), -1, dtype=torch.int32, device=x_dev.device)
         ends = torch.empty((admitted_b,), dtype=torch.int32, device=x_dev.device)
@@ -466,33 +472,50 @@ class XPUTrellisEncoder:
 
     def encode_tensor(self, tiles, pre_permute: bool = False, requested_b: Optional[int] = None,
                       traceback_mode: str = "gpu_resident", finalize: bool = True,
-                      allocator_hook: Optional[Callable[[int], None]] = None) -> dict:
+                      allocator_hook: Optional[Callable[[int], None]] = None,
+                      synchronize: bool = True, nan_count=None) -> dict:
         """Encode an (n, L) float32 device tensor, keeping every output on the
         device. Returns a dict of device tensors: ``x`` (kernel-order fp16
         inputs as f32), ``reconstructed_perm`` (f32, kernel order),
         ``indices`` (int16 states), and with ``finalize``: ``packed``,
         ``path_cost``, ``distortion``, ``reconstructed`` (fp16 bits as int16,
-        original order)."""
+        original order).
+
+        NaN inputs are counted by the prepare kernel. Without ``nan_count`` the
+        count is read back at once and a NaN raises ``ValueError`` before any
+        encoding. With ``nan_count`` (device int32) the count accumulates
+        there and the caller checks it later; the batch is encoded anyway
+        (its outputs are meaningless, every index stays a valid state).
+        ``synchronize=False`` (``gpu_resident`` only) launches everything on
+        the current stream and returns without waiting: host ``timings`` stay
+        zero and the scratch buffers are reused in stream order."""
         import torch
 
         if not isinstance(tiles, torch.Tensor) or tiles.device.type != "cuda":
             raise ValueError("encode_tensor expects a GPU tensor")
         n, width = self._flatten(tiles.shape)
         self._check_mode(n, width, pre_permute, traceback_mode)
+        if not synchronize and traceback_mode != "gpu_resident":
+            raise ValueError("synchronize=False requires traceback_mode='gpu_resident'")
         raw = tiles.reshape(n, width).to(torch.float32).contiguous()
-        if torch.isnan(raw).any().item():
-            raise ValueError("NaN tile values are not supported (see module docstring)")
         ext = build_quantize_extension()
         timings = {"search": 0.0, "traceback": 0.0}
         x = torch.empty_like(raw)
-        ext.prepare_tiles(raw, x, pre_permute)
+        if nan_count is None:
+            counter = torch.zeros(1, dtype=torch.int32, device=raw.device)
+            ext.prepare_tiles(raw, x, pre_permute, counter)
+            if int(counter.item()):
+                raise ValueError("NaN tile values are not supported (see module docstring)")
+        else:
+            ext.prepare_tiles(raw, x, pre_permute, nan_count)
         desired_b = min(n, requested_b if requested_b is not None else self.arena.default_cap_b)
         temp_costs, temp_edges, admitted_b = self.arena.acquire(
-            k=self.K, tile_len=self.L, requested_b=desired_b, allocator_hook=allocator_hook)
+            k=self.K, tile_len=self.L, requested_b=desired_b, allocator_hook=allocator_hook,
+            synchronize_reuse=synchronize)
         out_w = torch.empty((n, self.L), dtype=torch.float32, device=raw.device)
         out_i = torch.empty((n, self.L), dtype=torch.int16, device=raw.device)
         num_chunks = self._run_chunks(ext, x, out_w, out_i, temp_costs, temp_edges, admitted_b,
-                                      traceback_mode, timings)
+                                      traceback_mode, timings, synchronize)
         res = {"x": x, "reconstructed_perm": out_w, "indices": out_i, "admitted_b": admitted_b,
                "num_chunks": num_chunks, "timings": timings}
         if finalize:
@@ -504,8 +527,9 @@ class XPUTrellisEncoder:
             recon = torch.empty((n, self.L), dtype=torch.int16, device=raw.device)
             ext.finalize_tiles(x, raw, out_w, out_i, packed, path_cost, distortion, recon,
                                self.K, pre_permute)
-            torch.cuda.synchronize(self.device_index)
-            timings["finalize"] = time.perf_counter() - tp
+            if synchronize:
+                torch.cuda.synchronize(self.device_index)
+                timings["finalize"] = time.perf_counter() - tp
             res.update(packed=packed, path_cost=path_cost, distortion=distortion,
                        reconstructed=recon)
         return res

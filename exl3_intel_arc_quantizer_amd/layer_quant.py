@@ -200,9 +200,8 @@ def quantize_linear_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: 
     ldl = block_ldl(H_work, block_size=block_size)
     fact_residual = compute_factorization_residual(H_work, ldl.cholesky)
 
-    sync = (lambda: torch.cuda.synchronize(device)) if device.type == "cuda" else None
     lq = ldlq(weight=reg.weight, L=ldl.transformed, encode_tiles=tile_encoder,
-              buf_size_k=buf_size_k, synchronize=sync)
+              buf_size_k=buf_size_k)
     w_hat = weight_from_quantized(lq.weight_q, reg.su, reg.sv)
 
     diff = W - w_hat

@@ -125,8 +125,14 @@ def ldlq(weight: torch.Tensor, L: torch.Tensor, encode_tiles: TileEncoder,
     """Bottom-up one-sided LDLQ (ldlq.py:163-309). ``weight`` (k, n) float32
     in the transformed basis and ``L`` (k, k) from :func:`block_ldl` are not
     modified. ``encode_tiles`` maps (tiles_n, 256) tensor-core-order tiles to
-    (reconstruction, int16 states); ``encoder_seconds`` accumulates its wall
-    time (device-synchronised when ``synchronize`` is given)."""
+    (reconstruction, int16 states).
+
+    ``encoder_seconds`` is the encoder's share: on a CUDA weight, the sum of
+    HIP-event intervals around each call on the current stream, read once
+    after the traversal, so nothing in the loop waits for the device; with
+    ``synchronize`` given, host wall time between two ``synchronize()``
+    calls around each call instead. An encoder exposing ``check_finite``
+    (the HIP adapter) is asked once at the end to raise on NaN inputs."""
     if weight.dim() != 2 or weight.dtype != torch.float32:
         raise ValueError(f"weight must be a 2-D float32 tensor, got {weight.dtype} "
                          f"{tuple(weight.shape)}")
@@ -155,6 +161,8 @@ def ldlq(weight: torch.Tensor, L: torch.Tensor, encode_tiles: TileEncoder,
     encoded = torch.zeros((tiles_k, tiles_n, 256), dtype=torch.int16, device=device)
     enc_s = 0.0
     calls = 0
+    use_events = synchronize is None and device.type == "cuda"
+    events = []
 
     for j in range(k, 0, -buf_size_k):
         i = j - buf_size_k
@@ -169,13 +177,21 @@ def ldlq(weight: torch.Tensor, L: torch.Tensor, encode_tiles: TileEncoder,
             rows = weight[r0:r1] + comp
             tiles = rows.reshape(16, tiles_n, 16).permute(1, 0, 2).reshape(tiles_n, 256)
             tiles = tiles[:, perm].contiguous()
-            if synchronize is not None:
+            if use_events:
+                ev0 = torch.cuda.Event(enable_timing=True)
+                ev0.record()
+            elif synchronize is not None:
                 synchronize()
             t0 = time.perf_counter()
             quant_w, quant_i = encode_tiles(tiles)
-            if synchronize is not None:
-                synchronize()
-            enc_s += time.perf_counter() - t0
+            if use_events:
+                ev1 = torch.cuda.Event(enable_timing=True)
+                ev1.record()
+                events.append((ev0, ev1))
+            else:
+                if synchronize is not None:
+                    synchronize()
+                enc_s += time.perf_counter() - t0
             calls += 1
             if tuple(quant_w.shape) != (tiles_n, 256) or tuple(quant_i.shape) != (tiles_n, 256):
                 raise ValueError("encode_tiles must return two (tiles_n, 256) tensors, got "
@@ -186,5 +202,11 @@ def ldlq(weight: torch.Tensor, L: torch.Tensor, encode_tiles: TileEncoder,
         # Span residual into the feedback of the spans above.
         prod_cache.addmm_(L[i:j].T, weight[i:j] - weight_q[i:j], alpha=1.0, beta=1.0)
 
+    if events:
+        events[-1][1].synchronize()
+        enc_s = sum(a.elapsed_time(b) for a, b in events) / 1e3
+    check_finite = getattr(encode_tiles, "check_finite", None)
+    if check_finite is not None:
+        check_finite()
     return LDLQResult(weight_q=weight_q, encoded=encoded, tiles_k=tiles_k, tiles_n=tiles_n,
                       buf_size_k=buf_size_k, encoder_seconds=enc_s, encoder_calls=calls)

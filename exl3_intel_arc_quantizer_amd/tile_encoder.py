@@ -12,6 +12,13 @@ back (ldlq.py:370-380), this one keeps a CUDA input on the device: the
 encoder's ``encode_tensor`` runs the HIP path and the outputs stay in HBM.
 A CPU input is copied to the encoder's device and the outputs are returned
 on the input's device.
+
+A CUDA input is encoded without any device-to-host round trip: the kernels
+are queued on the current stream and the call returns, so the LDLQ loop's
+host work overlaps the encoder. NaN inputs are counted on the device and
+reported by ``encode.check_finite()``, which raises ``ValueError`` if any
+call since the previous check saw one (``ldlq`` calls it when its traversal
+ends). With ``asynchronous=False`` every call checks at once instead.
 """
 
 from __future__ import annotations
@@ -25,31 +32,50 @@ TileEncoder = Callable[["object"], "tuple"]
 
 def make_xpu_tile_encoder(K: int = 2, device_index: int = 0, arena=None, sg_size: int = 32,
                           force_global_costs: bool = False,
-                          traceback_mode: str = "gpu_resident") -> TileEncoder:
+                          traceback_mode: str = "gpu_resident",
+                          asynchronous: bool = True) -> TileEncoder:
     """MI355X tile encoder (``XPUTrellisEncoder``, MUL1 codebook) as an LDLQ
     callback. The encoder and its ScratchArena are created once and reused
     for every call (ldlq.py:352-357)."""
+    import torch
+
     from .gpu_quantizer import XPUTrellisEncoder
 
     encoder = XPUTrellisEncoder(K=K, cb=CB_MUL1, arena=arena, device_index=device_index,
                                 sg_size=sg_size, force_global_costs=force_global_costs)
+    run_async = asynchronous and traceback_mode == "gpu_resident"
+    state = {"nan_count": None}
+
+    def check_finite() -> None:
+        counter = state["nan_count"]
+        if counter is None:
+            return
+        seen = int(counter.item())
+        if seen:
+            counter.zero_()
+            raise ValueError(f"NaN tile values are not supported ({seen} seen by the encoder)")
 
     def encode(tiles):
-        import torch
-
         if tiles.dim() != 2 or tiles.size(1) != 256:
             raise ValueError(f"expected (tiles_n, 256) tiles, got {tuple(tiles.shape)}")
         dev_tiles = tiles.detach().to(device=f"cuda:{device_index}", dtype=torch.float32)
+        on_device = tiles.device == dev_tiles.device
+        if run_async and state["nan_count"] is None:
+            state["nan_count"] = torch.zeros(1, dtype=torch.int32, device=dev_tiles.device)
         res = encoder.encode_tensor(dev_tiles.contiguous(), pre_permute=False,
-                                    traceback_mode=traceback_mode, finalize=False)
+                                    traceback_mode=traceback_mode, finalize=False,
+                                    synchronize=not run_async,
+                                    nan_count=state["nan_count"] if run_async else None)
         recon, idx = res["reconstructed_perm"], res["indices"]
-        if tiles.device != recon.device:
+        if not on_device:
             recon, idx = recon.to(tiles.device), idx.to(tiles.device)
+            check_finite()
         return recon, idx
 
     encode.K = K
     encode.cb = CB_MUL1
     encode.encoder = encoder
+    encode.check_finite = check_finite
     return encode
 
 

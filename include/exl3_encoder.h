@@ -100,9 +100,12 @@ int exl3_backward_pass(const uint16_t* temp_costs, const uint8_t* temp_edges, fl
 
 /* Host-side preparation of the reference wrapper (xpu_quantizer.py:649-655)
  * on the device: out[t][i] = fp16-rounded raw[t][perm[i]] (permute = 1,
- * tensor-core permutation, L = 256) or raw[t][i] (permute = 0), as f32. */
+ * tensor-core permutation, L = 256) or raw[t][i] (permute = 0), as f32.
+ * nan_count (device int32, may be NULL) is incremented once per NaN input
+ * value; the reference's NaN behaviour is not reproduced, callers reject
+ * batches with a non-zero count. */
 int exl3_prepare_tiles(const float* raw, float* out, int64_t n, int L, int permute,
-                       void* stream);
+                       int32_t* nan_count, void* stream);
 
 /* Host-side post-processing of the reference wrapper
  * (xpu_quantizer.py:926-976) on the device, per tile:

@@ -131,3 +131,37 @@ def test_quantize_decoder_layer_shared_arena(torch_mod):
         assert np.isfinite(r.metrics.proxy_loss) and 0 < r.metrics.normalized_proxy_loss < 0.5
         k, n = r.original_shape
         assert r.encoded.shape == (k // 16, n // 16, 256)
+
+
+def test_ldlq_async_encoder_timing_and_nan(torch_mod):
+    """The traversal queues every encoder call without waiting: the encoder
+    share comes from HIP events (positive, below the wall time), states equal
+    those of a synchronised traversal, and a NaN reaching the encoder raises
+    when the traversal ends."""
+    import time
+
+    from exl3_intel_arc_quantizer_amd.ldlq import block_ldl, ldlq
+    from exl3_intel_arc_quantizer_amd.tile_encoder import make_xpu_tile_encoder
+    torch = torch_mod
+    rng = np.random.default_rng(41)
+    W = torch.from_numpy(rng.standard_normal((256, 256)).astype(np.float32)).cuda()
+    _, X = _layer_case(256, 256, 42)
+    Xc = torch.from_numpy(X).cuda()
+    L = block_ldl((Xc.T @ Xc) / X.shape[0] + 0.1 * torch.eye(256, device="cuda")).transformed
+    enc = make_xpu_tile_encoder(K=2)
+    try:
+        t0 = time.perf_counter()
+        fast = ldlq(W, L, enc)
+        wall = time.perf_counter() - t0
+        assert fast.encoder_calls == 16 and 0.0 < fast.encoder_seconds < wall
+        slow = ldlq(W, L, make_xpu_tile_encoder(K=2, asynchronous=False),
+                    synchronize=torch.cuda.synchronize)
+        assert torch.equal(fast.encoded, slow.encoded)
+        assert torch.equal(fast.weight_q, slow.weight_q)
+        W_bad = W.clone()
+        W_bad[200, 3] = float("nan")
+        with pytest.raises(ValueError, match="NaN"):
+            ldlq(W_bad, L, enc)
+        enc.check_finite()
+    finally:
+        enc.encoder.arena.release()

@@ -278,6 +278,36 @@ def test_tile_encoder_adapter(torch_mod):
         enc.encoder.arena.release()
 
 
+def test_tile_encoder_nan_rejection(torch_mod):
+    """NaN tiles are rejected (a documented deviation): at once by
+    encode_tensor, and by the asynchronous adapter at check_finite(), which
+    also resets its count; the batches queued before it stay valid."""
+    from exl3_intel_arc_quantizer_amd.tile_encoder import make_xpu_tile_encoder
+    rng = np.random.default_rng(77)
+    good = rng.normal(0.0, 1.0, size=(3, 256)).astype(np.float32)
+    bad = good.copy()
+    bad[1, 17] = np.nan
+    ref = c_oracle.encode_tiles(good.astype(np.float16).astype(np.float32), K=3, cb=2,
+                                pre_permute=False)
+    enc = make_xpu_tile_encoder(K=3)
+    try:
+        with pytest.raises(ValueError, match="NaN"):
+            enc.encoder.encode_tensor(torch_mod.from_numpy(bad).cuda(), finalize=False)
+        _, idx_good = enc(torch_mod.from_numpy(good).cuda())
+        enc(torch_mod.from_numpy(bad).cuda())           # queued, not checked yet
+        _, idx_after = enc(torch_mod.from_numpy(good).cuda())
+        with pytest.raises(ValueError, match="1 seen"):
+            enc.check_finite()
+        enc.check_finite()                               # count was reset
+        for idx in (idx_good, idx_after):
+            np.testing.assert_array_equal(idx.cpu().numpy().view(np.uint16), ref.output_indices)
+        # A CPU input is copied back, so the adapter checks at once.
+        with pytest.raises(ValueError, match="NaN"):
+            enc(torch_mod.from_numpy(bad))
+    finally:
+        enc.encoder.arena.release()
+
+
 def test_traceback_modes_and_variants_agree():
     """tests/test_xpu_quantizer.py:299-330."""
     rng = np.random.default_rng(909)

@@ -101,5 +101,5 @@ def test_forward_and_backward_reject_bad_arguments():
     assert "num_tiles" in lib.exl3_last_error().decode()
     assert lib.exl3_decode_codebook(5, None, None) != 0
     assert lib.exl3_pack_trellis(None, None, 0, 2, None) != 0
-    assert lib.exl3_prepare_tiles(None, None, 1, 160, 1, None) != 0
+    assert lib.exl3_prepare_tiles(None, None, 1, 160, 1, None, None) != 0
     assert "pre_permute" in lib.exl3_last_error().decode()
