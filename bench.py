@@ -240,7 +240,7 @@ def run_layer_config(torch, K=4):
                                "(tests/test_gpu_layer.py); a full-size CPU run is hours"}
 
 
-def run_decoder_config(torch, K=4, cpu_tiles_per_s=None):
+def run_decoder_config(torch, K=4, cpu_tiles_per_s=None, lockstep=True):
     """configs[4]: a 9B-class decoder layer (hidden 4096; q, o 4096x4096;
     k, v 1024x4096; gate, up 12288x4096; down 4096x12288), random-init weights
     (torch seed 5), Hessians per shared-input group from synthetic bf16
@@ -263,27 +263,38 @@ def run_decoder_config(torch, K=4, cpu_tiles_per_s=None):
     layer = layer.cuda()
     names = [n for n, m in layer.named_modules() if isinstance(m, nn.Linear)]
     hess = {}
-    t0 = time.perf_counter()
+    t_hess = 0.0
     for seed, (key, members) in enumerate(hessian_groups(names).items(), start=6):
         width = 12288 if key == "mlp.down_proj" else 4096
         X = torch.from_numpy(_synthetic_activations(np.random.default_rng(seed), 16384, width))
-        H, _ = hessian_from_activations(X.to(torch.bfloat16).cuda())
+        X = X.to(torch.bfloat16).cuda()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        H, _ = hessian_from_activations(X)
+        torch.cuda.synchronize()
+        t_hess += time.perf_counter() - t0
         for mname in members:
             hess[mname] = H
-    torch.cuda.synchronize()
-    t_hess = time.perf_counter() - t0
-    rep = quantize_decoder_layer(layer, hess, K=K)
+    # A model conversion runs this once per layer; the first layer of a
+    # process also pays rocSOLVER / hipBLASLt kernel loading, so the timed
+    # run is the second conversion of the same shapes (the steady state).
+    first = quantize_decoder_layer(layer, hess, K=K, lockstep=lockstep)
+    first_wall = first.total_elapsed_seconds
+    del first
+    rep = quantize_decoder_layer(layer, hess, K=K, lockstep=lockstep)
     wall = rep.total_elapsed_seconds
     calls = sum(r.metrics.encoder_calls for r in rep.module_results.values())
     out = {"metric": "9B-class decoder layer conversion, K=4, 1 MI355X: wall time",
            "value": round(wall, 3), "unit": "s", "higher_is_better": False, "n_gpus": 1,
            "dtype": "fp16", "data": "synthetic",
            "config": {"workload": "configs[4]", "K": K, "tiles": rep.tiles,
-                      "encoder_calls": calls},
+                      "module_encoder_calls": calls, "lockstep": lockstep},
            "tiles_per_s": round(rep.tiles / wall, 1),
            "encoder_seconds": round(rep.encoder_seconds, 3),
            "encoder_share": round(rep.encoder_seconds / wall, 4),
            "hessian_seconds": round(t_hess, 3),
+           "first_layer_seconds": round(first_wall, 3),
+           "phases": {k: round(v, 3) for k, v in rep.extra.items() if k.endswith("_seconds")},
            "total_proxy_loss": rep.total_proxy_loss, "mean_mse": rep.mean_mse,
            "peak_device_memory_bytes": rep.peak_device_memory_bytes,
            "modules": {n: {"shape_kn": list(r.original_shape),
@@ -312,6 +323,8 @@ def main() -> int:
                     help="configs[3]: LDLQ-driven 4096x4096 layer (prints its own JSON line)")
     ap.add_argument("--decoder", action="store_true",
                     help="configs[4]: 9B-class decoder layer conversion (its own JSON line)")
+    ap.add_argument("--sequential", action="store_true",
+                    help="with --decoder: one projection at a time (the reference's order)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device copy (known-size kernel for PMC byte "
                          "counter calibration)")
@@ -331,7 +344,8 @@ def main() -> int:
         if args.decoder and not args.no_cpu_baseline:
             cpu = cpu_baseline(tiles, 4)
         line = (run_layer_config(torch) if args.layer else
-                run_decoder_config(torch, cpu_tiles_per_s=cpu["value"] if cpu else None))
+                run_decoder_config(torch, cpu_tiles_per_s=cpu["value"] if cpu else None,
+                                   lockstep=not args.sequential))
         print(json.dumps(line), flush=True)
         return 0
     if not args.no_cpu_baseline and not args.profile_forward:

@@ -27,7 +27,8 @@ import torch
 
 from .hadamard import HAD_DIM, blockwise_preapply_had_l_, blockwise_preapply_had_r_, \
     weight_from_quantized
-from .ldlq import DEFAULT_BLOCK_SIZE, DEFAULT_BUF_SIZE_K, BlockLDLResult, block_ldl, ldlq
+from .ldlq import (DEFAULT_BLOCK_SIZE, DEFAULT_BUF_SIZE_K, BlockLDLResult, LDLQResult,
+                   block_ldl, ldlq, ldlq_lockstep)
 from .regularize import RegularizeResult, regularize
 from .tile_encoder import TileEncoder, make_xpu_tile_encoder
 from .trellis_format import CB_MUL1
@@ -160,13 +161,24 @@ def compute_proxy_loss(W: torch.Tensor, W_hat: torch.Tensor,
 
 # -------------------------------------------------------------------- driver
 
-def quantize_linear_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int = 2,
-                           cb: int = CB_MUL1, tile_encoder: Optional[TileEncoder] = None,
-                           skip_g_scale: bool = True, buf_size_k: int = DEFAULT_BUF_SIZE_K,
-                           block_size: int = DEFAULT_BLOCK_SIZE) -> QuantizedModuleResult:
-    """Quantise one linear weight with LDLQ (layer_quant.py:130-265). The
-    weight is (out, in) as in ``nn.Linear`` or already (in, out) = (k, n);
-    ``H`` is (in, in). Runs on the device of ``H``, which must be a GPU."""
+@dataclass
+class _PreparedModule:
+    """A projection between regularisation and LDLQ."""
+
+    name: str
+    W: torch.Tensor            # (k, n) float32, original basis
+    H: torch.Tensor
+    reg: RegularizeResult
+    ldl: BlockLDLResult
+    fact_residual: float
+    prep_seconds: float
+
+
+def _prepare_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int,
+                    tile_encoder: Optional[TileEncoder], skip_g_scale: bool,
+                    block_size: int) -> _PreparedModule:
+    """Shape checks, regularisation, Hessian rotation and block LDL
+    (layer_quant.py:130-214)."""
     t0 = time.time()
     if weight.dim() != 2:
         raise ValueError(f"weight must be 2D, got shape {tuple(weight.shape)}")
@@ -181,9 +193,7 @@ def quantize_linear_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: 
     else:
         raise ValueError(f"Weight shape {tuple(weight.shape)} does not match Hessian dim {k_dim}")
     k, n = W.shape
-    if tile_encoder is None:
-        tile_encoder = make_xpu_tile_encoder(K=K, device_index=device.index or 0)
-    enc_k = getattr(tile_encoder, "K", None)
+    enc_k = getattr(tile_encoder, "K", None) if tile_encoder is not None else None
     if enc_k is not None and enc_k != K:
         raise ValueError(f"Tile encoder K={enc_k} does not match the requested K={K}.")
     if not skip_g_scale:
@@ -199,35 +209,67 @@ def quantize_linear_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: 
     blockwise_preapply_had_r_(H_work, HAD_DIM)
     ldl = block_ldl(H_work, block_size=block_size)
     fact_residual = compute_factorization_residual(H_work, ldl.cholesky)
+    return _PreparedModule(name=name, W=W, H=H, reg=reg, ldl=ldl, fact_residual=fact_residual,
+                           prep_seconds=time.time() - t0)
 
-    lq = ldlq(weight=reg.weight, L=ldl.transformed, encode_tiles=tile_encoder,
-              buf_size_k=buf_size_k)
+
+def _finish_module(pm: _PreparedModule, lq: LDLQResult, K: int, cb: int,
+                   shared_seconds: float) -> QuantizedModuleResult:
+    """Back to the original basis and the metrics (layer_quant.py:216-265);
+    ``elapsed_seconds`` = preparation + ``shared_seconds`` + this step."""
+    t0 = time.time()
+    W, reg = pm.W, pm.reg
     w_hat = weight_from_quantized(lq.weight_q, reg.su, reg.sv)
-
     diff = W - w_hat
-    proxy, norm_proxy = compute_proxy_loss(W, w_hat, H)
+    proxy, norm_proxy = compute_proxy_loss(W, w_hat, pm.H)
     metrics = ModuleMetrics(
         mse=float(diff.pow(2).mean().item()),
         relative_frobenius_error=float(torch.linalg.norm(diff).item()
                                        / max(1e-12, torch.linalg.norm(W).item())),
         tile_distortion=float((reg.weight - lq.weight_q).pow(2).mean().item()),
         proxy_loss=proxy, normalized_proxy_loss=norm_proxy,
-        factorization_residual=fact_residual, retries=ldl.retries, g_scale=reg.g_scale,
-        elapsed_seconds=time.time() - t0, encoder_seconds=lq.encoder_seconds,
-        encoder_calls=lq.encoder_calls)
-    return QuantizedModuleResult(name=name, K=K, cb=cb, original_shape=(k, n), weight_orig=W,
-                                 w_hat=w_hat, encoded=lq.encoded, su=reg.su, sv=reg.sv,
-                                 metrics=metrics, regularize_result=reg, ldl_result=ldl)
+        factorization_residual=pm.fact_residual, retries=pm.ldl.retries, g_scale=reg.g_scale,
+        elapsed_seconds=pm.prep_seconds + shared_seconds + (time.time() - t0),
+        encoder_seconds=lq.encoder_seconds, encoder_calls=lq.encoder_calls)
+    return QuantizedModuleResult(name=pm.name, K=K, cb=cb, original_shape=tuple(W.shape),
+                                 weight_orig=W, w_hat=w_hat, encoded=lq.encoded, su=reg.su,
+                                 sv=reg.sv, metrics=metrics, regularize_result=reg,
+                                 ldl_result=pm.ldl)
+
+
+def quantize_linear_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int = 2,
+                           cb: int = CB_MUL1, tile_encoder: Optional[TileEncoder] = None,
+                           skip_g_scale: bool = True, buf_size_k: int = DEFAULT_BUF_SIZE_K,
+                           block_size: int = DEFAULT_BLOCK_SIZE) -> QuantizedModuleResult:
+    """Quantise one linear weight with LDLQ (layer_quant.py:130-265). The
+    weight is (out, in) as in ``nn.Linear`` or already (in, out) = (k, n);
+    ``H`` is (in, in). Runs on the device of ``H``, which must be a GPU."""
+    pm = _prepare_module(name, weight, H, K, tile_encoder, skip_g_scale, block_size)
+    if tile_encoder is None:
+        tile_encoder = make_xpu_tile_encoder(K=K, device_index=H.device.index or 0)
+    t0 = time.time()
+    lq = ldlq(weight=pm.reg.weight, L=pm.ldl.transformed, encode_tiles=tile_encoder,
+              buf_size_k=buf_size_k)
+    return _finish_module(pm, lq, K, cb, time.time() - t0)
 
 
 def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Tensor], K: int = 2,
                            cb: int = CB_MUL1, device: Optional[torch.device] = None,
                            skip_g_scale: bool = True, buf_size_k: int = DEFAULT_BUF_SIZE_K,
                            block_size: int = DEFAULT_BLOCK_SIZE, memory_policy=None,
-                           module_names: Optional[List[str]] = None) -> LayerQuantizationReport:
+                           module_names: Optional[List[str]] = None,
+                           lockstep: bool = True) -> LayerQuantizationReport:
     """Quantise every bias-free ``nn.Linear`` of a decoder layer (or the
     ``module_names`` subset) with one shared encoder and scratch arena
-    (layer_quant.py:268-387)."""
+    (layer_quant.py:268-387).
+
+    With ``lockstep`` (the default) the projections are prepared first and
+    their LDLQ traversals run side by side (``ldlq_lockstep``): each encoder
+    launch carries block b of every projection, e.g. 2176 tiles for
+    q/k/v/o/gate/up of a 4096-wide layer instead of 64 to 768. The results
+    equal the one-at-a-time order (``lockstep=False``, the reference's); a
+    module's ``elapsed_seconds`` then includes the shared traversal and its
+    ``encoder_seconds`` is its tile share of each call."""
     from .gpu_quantizer import ScratchArena
     from .memory_policy import MemoryPolicy
 
@@ -245,17 +287,34 @@ def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Ten
     missing = [n for n in selected if n not in available]
     if missing:
         raise KeyError(f"requested modules are not bias-free nn.Linear submodules: {missing}")
+    for name in selected:
+        if name not in hessians:
+            raise KeyError(f"Hessian missing for module {name}")
     torch.cuda.reset_peak_memory_stats(device)
     results: Dict[str, QuantizedModuleResult] = {}
+    phases: Dict[str, float] = {}
     try:
-        for name in selected:
-            if name not in hessians:
-                raise KeyError(f"Hessian missing for module {name}")
-            results[name] = quantize_linear_module(
-                name=name, weight=available[name].weight.data, H=hessians[name].to(device),
-                K=K, cb=cb, tile_encoder=encoder, skip_g_scale=skip_g_scale,
-                buf_size_k=buf_size_k, block_size=block_size)
+        if lockstep:
+            tp = time.time()
+            prepared = [_prepare_module(name, available[name].weight.data,
+                                        hessians[name].to(device), K, encoder, skip_g_scale,
+                                        block_size) for name in selected]
             torch.cuda.synchronize(device)
+            t0 = time.time()
+            lqs = ldlq_lockstep([(pm.reg.weight, pm.ldl.transformed) for pm in prepared],
+                                encoder, buf_size_k=buf_size_k)
+            shared = time.time() - t0
+            for pm, lq in zip(prepared, lqs):
+                results[pm.name] = _finish_module(pm, lq, K, cb, shared)
+            phases = {"prepare_seconds": t0 - tp, "traversal_seconds": shared,
+                      "finish_seconds": time.time() - t0 - shared}
+        else:
+            for name in selected:
+                results[name] = quantize_linear_module(
+                    name=name, weight=available[name].weight.data, H=hessians[name].to(device),
+                    K=K, cb=cb, tile_encoder=encoder, skip_g_scale=skip_g_scale,
+                    buf_size_k=buf_size_k, block_size=block_size)
+                torch.cuda.synchronize(device)
     finally:
         arena.release()
     tiles = sum(r.original_shape[0] * r.original_shape[1] // 256 for r in results.values())
@@ -266,4 +325,5 @@ def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Ten
         mean_mse=float(sum(r.metrics.mse for r in results.values()) / max(1, len(results))),
         peak_device_memory_bytes=int(torch.cuda.max_memory_allocated(device)),
         scratch_arena_reused=True, device_index=device.index or 0, tiles=tiles,
-        encoder_seconds=sum(r.metrics.encoder_seconds for r in results.values()))
+        encoder_seconds=sum(r.metrics.encoder_seconds for r in results.values()),
+        extra={"lockstep": bool(lockstep), **phases})

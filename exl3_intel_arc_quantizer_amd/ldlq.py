@@ -15,13 +15,18 @@ order, go through the tile encoder (the HIP encoder, tiles staying in HBM),
 and the reconstruction is un-permuted into ``weight_q`` while the states stay
 in tensor-core order. After a span its residual is propagated into
 ``prod_cache`` for the spans above. All of it runs on the weight's device.
+
+A traversal is a chain of n / 16-tile encoder calls (256 tiles for a 4096
+wide projection: one workgroup per CU, half the encoder's occupancy).
+``ldlq_lockstep`` walks independent projections side by side and encodes
+their blocks in one call per step.
 """
 
 from __future__ import annotations
 
 import time
 from dataclasses import dataclass, field
-from typing import Callable
+from typing import Callable, List, Optional, Sequence, Tuple
 
 import torch
 
@@ -34,7 +39,7 @@ DEFAULT_MAX_RETRIES = 10
 DEFAULT_BUF_SIZE_K = 128
 
 __all__ = ["DEFAULT_BLOCK_SIZE", "DEFAULT_SIGMA_REG", "DEFAULT_MAX_RETRIES", "DEFAULT_BUF_SIZE_K",
-           "BlockLDLResult", "block_ldl", "LDLQResult", "ldlq", "TileEncoder",
+           "BlockLDLResult", "block_ldl", "LDLQResult", "ldlq", "ldlq_lockstep", "TileEncoder",
            "make_xpu_tile_encoder", "make_gpu_tile_encoder"]
 
 
@@ -119,6 +124,127 @@ def _as_int16_states(indices: torch.Tensor) -> torch.Tensor:
     return torch.where(values >= 0x8000, values - 0x10000, values).to(torch.int16)
 
 
+class _Traversal:
+    """One weight's bottom-up LDLQ walk, block by block: ``tiles(b)`` forms
+    block b's encoder input, ``store(b, ...)`` takes its result and, after a
+    span's last block, feeds the span residual into ``prod_cache``."""
+
+    def __init__(self, weight: torch.Tensor, L: torch.Tensor, buf_size_k: int):
+        if weight.dim() != 2 or weight.dtype != torch.float32:
+            raise ValueError(f"weight must be a 2-D float32 tensor, got {weight.dtype} "
+                             f"{tuple(weight.shape)}")
+        k, n = weight.shape
+        if k % 16 != 0:
+            raise ValueError(f"rows ({k}) must be a multiple of 16")
+        if n % 128 != 0:
+            raise ValueError(f"columns ({n}) must be a multiple of 128")
+        if L.dim() != 2 or tuple(L.shape) != (k, k) or L.dtype != torch.float32:
+            raise ValueError(f"L must be a float32 ({k}, {k}) tensor, got {L.dtype} "
+                             f"{tuple(L.shape)}")
+        if L.device != weight.device:
+            raise ValueError(f"L and weight must be on the same device, got {L.device} / "
+                             f"{weight.device}")
+        buf_size_k = int(buf_size_k)
+        if buf_size_k < 16 or buf_size_k % 16 != 0:
+            raise ValueError(f"buf_size_k must be a positive multiple of 16, got {buf_size_k}")
+        if n % buf_size_k != 0 or k % buf_size_k != 0:
+            raise ValueError(f"rows ({k}) and columns ({n}) must be divisible by buf_size_k "
+                             f"({buf_size_k})")
+        device = weight.device
+        self.weight, self.L, self.buf_size_k = weight, L, buf_size_k
+        self.tiles_k, self.tiles_n, self.n = k // 16, n // 16, n
+        self.perm = torch.as_tensor(tensor_core_perm(), dtype=torch.long, device=device)
+        self.inv_perm = torch.as_tensor(tensor_core_perm_inv(), dtype=torch.long, device=device)
+        self.prod_cache = torch.zeros((k, n), dtype=torch.float32, device=device)
+        self.weight_q = torch.zeros((k, n), dtype=torch.float32, device=device)
+        self.encoded = torch.zeros((k // 16, n // 16, 256), dtype=torch.int16, device=device)
+        # (span start i, span end j, first row r0) in traversal order: spans
+        # from the last, 16-row blocks inside a span from the last.
+        self.blocks = [(j - buf_size_k, j, j - buf_size_k + bj - 16)
+                       for j in range(k, 0, -buf_size_k) for bj in range(buf_size_k, 0, -16)]
+        self.encoder_seconds = 0.0
+        self.encoder_calls = 0
+
+    def tiles(self, b: int) -> torch.Tensor:
+        i, j, r0 = self.blocks[b]
+        r1 = r0 + 16
+        comp = self.prod_cache[r0:r1]
+        if r1 < j:
+            # Rows already quantised below, within this span.
+            err = self.weight[r1:j] - self.weight_q[r1:j]
+            comp.addmm_(self.L[r1:j, r0:r1].T, err, alpha=1.0, beta=1.0)
+        rows = self.weight[r0:r1] + comp
+        tiles = rows.reshape(16, self.tiles_n, 16).permute(1, 0, 2).reshape(self.tiles_n, 256)
+        return tiles[:, self.perm].contiguous()
+
+    def store(self, b: int, quant_w: torch.Tensor, quant_i: torch.Tensor) -> None:
+        i, j, r0 = self.blocks[b]
+        device = self.weight.device
+        if tuple(quant_w.shape) != (self.tiles_n, 256) or tuple(quant_i.shape) != (self.tiles_n, 256):
+            raise ValueError("encode_tiles must return two (tiles_n, 256) tensors, got "
+                             f"{tuple(quant_w.shape)} / {tuple(quant_i.shape)}")
+        quant_w = quant_w.to(device=device, dtype=torch.float32)[:, self.inv_perm]
+        self.weight_q[r0:r0 + 16] = (quant_w.reshape(self.tiles_n, 16, 16).permute(1, 0, 2)
+                                     .reshape(16, self.n))
+        self.encoded[r0 // 16] = _as_int16_states(quant_i.to(device=device))
+        if r0 == i:
+            # Span residual into the feedback of the spans above.
+            self.prod_cache.addmm_(self.L[i:j].T, self.weight[i:j] - self.weight_q[i:j],
+                                   alpha=1.0, beta=1.0)
+
+    def result(self) -> "LDLQResult":
+        return LDLQResult(weight_q=self.weight_q, encoded=self.encoded, tiles_k=self.tiles_k,
+                          tiles_n=self.tiles_n, buf_size_k=self.buf_size_k,
+                          encoder_seconds=self.encoder_seconds,
+                          encoder_calls=self.encoder_calls)
+
+
+def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
+                  synchronize: Optional[Callable[[], None]]) -> None:
+    """Step every walk's block b through one encoder call per b."""
+    use_events = synchronize is None and walks[0].weight.device.type == "cuda"
+    pending = []      # (event pair, [(walk, tiles)]) read after the loop
+    for b in range(max(len(w.blocks) for w in walks)):
+        active = [w for w in walks if b < len(w.blocks)]
+        parts = [w.tiles(b) for w in active]
+        batch = parts[0] if len(parts) == 1 else torch.cat(parts)
+        if use_events:
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev0.record()
+        elif synchronize is not None:
+            synchronize()
+        t0 = time.perf_counter()
+        quant_w, quant_i = encode_tiles(batch)
+        if use_events:
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev1.record()
+            pending.append(((ev0, ev1), [(w, w.tiles_n) for w in active]))
+        else:
+            if synchronize is not None:
+                synchronize()
+            dt = time.perf_counter() - t0
+            for w in active:
+                w.encoder_seconds += dt * w.tiles_n / batch.shape[0]
+        if tuple(quant_w.shape) != (batch.shape[0], 256) or tuple(quant_i.shape) != (batch.shape[0], 256):
+            raise ValueError("encode_tiles must return two (tiles_n, 256) tensors, got "
+                             f"{tuple(quant_w.shape)} / {tuple(quant_i.shape)}")
+        off = 0
+        for w in active:
+            w.store(b, quant_w[off:off + w.tiles_n], quant_i[off:off + w.tiles_n])
+            w.encoder_calls += 1
+            off += w.tiles_n
+    if pending:
+        pending[-1][0][1].synchronize()
+        for (ev0, ev1), members in pending:
+            dt = ev0.elapsed_time(ev1) / 1e3
+            total = sum(t for _, t in members)
+            for w, t in members:
+                w.encoder_seconds += dt * t / total
+    check_finite = getattr(encode_tiles, "check_finite", None)
+    if check_finite is not None:
+        check_finite()
+
+
 def ldlq(weight: torch.Tensor, L: torch.Tensor, encode_tiles: TileEncoder,
          buf_size_k: int = DEFAULT_BUF_SIZE_K,
          synchronize: Callable[[], None] = None) -> LDLQResult:
@@ -127,86 +253,37 @@ def ldlq(weight: torch.Tensor, L: torch.Tensor, encode_tiles: TileEncoder,
     modified. ``encode_tiles`` maps (tiles_n, 256) tensor-core-order tiles to
     (reconstruction, int16 states).
 
+    Bottom-up: spans of ``buf_size_k`` rows from the last, 16-row blocks
+    inside a span from the last. A block's rows get the compensation of the
+    rows already quantised below it in the span (``addmm`` against the
+    strictly lower slice of L) plus the span-level feedback ``prod_cache``;
+    after a span its residual is propagated into ``prod_cache``.
+
     ``encoder_seconds`` is the encoder's share: on a CUDA weight, the sum of
     HIP-event intervals around each call on the current stream, read once
     after the traversal, so nothing in the loop waits for the device; with
     ``synchronize`` given, host wall time between two ``synchronize()``
     calls around each call instead. An encoder exposing ``check_finite``
     (the HIP adapter) is asked once at the end to raise on NaN inputs."""
-    if weight.dim() != 2 or weight.dtype != torch.float32:
-        raise ValueError(f"weight must be a 2-D float32 tensor, got {weight.dtype} "
-                         f"{tuple(weight.shape)}")
-    k, n = weight.shape
-    if k % 16 != 0:
-        raise ValueError(f"rows ({k}) must be a multiple of 16")
-    if n % 128 != 0:
-        raise ValueError(f"columns ({n}) must be a multiple of 128")
-    if L.dim() != 2 or tuple(L.shape) != (k, k) or L.dtype != torch.float32:
-        raise ValueError(f"L must be a float32 ({k}, {k}) tensor, got {L.dtype} {tuple(L.shape)}")
-    if L.device != weight.device:
-        raise ValueError(f"L and weight must be on the same device, got {L.device} / {weight.device}")
-    buf_size_k = int(buf_size_k)
-    if buf_size_k < 16 or buf_size_k % 16 != 0:
-        raise ValueError(f"buf_size_k must be a positive multiple of 16, got {buf_size_k}")
-    if n % buf_size_k != 0 or k % buf_size_k != 0:
-        raise ValueError(f"rows ({k}) and columns ({n}) must be divisible by buf_size_k "
-                         f"({buf_size_k})")
+    walk = _Traversal(weight, L, buf_size_k)
+    _run_lockstep([walk], encode_tiles, synchronize)
+    return walk.result()
 
-    device = weight.device
-    tiles_k, tiles_n = k // 16, n // 16
-    perm = torch.as_tensor(tensor_core_perm(), dtype=torch.long, device=device)
-    inv_perm = torch.as_tensor(tensor_core_perm_inv(), dtype=torch.long, device=device)
-    prod_cache = torch.zeros((k, n), dtype=torch.float32, device=device)
-    weight_q = torch.zeros((k, n), dtype=torch.float32, device=device)
-    encoded = torch.zeros((tiles_k, tiles_n, 256), dtype=torch.int16, device=device)
-    enc_s = 0.0
-    calls = 0
-    use_events = synchronize is None and device.type == "cuda"
-    events = []
 
-    for j in range(k, 0, -buf_size_k):
-        i = j - buf_size_k
-        for bj in range(buf_size_k, 0, -16):
-            bi = bj - 16
-            r0, r1 = i + bi, i + bj           # the 16 rows being quantised
-            comp = prod_cache[r0:r1]
-            if r1 < j:
-                # Rows already quantised below, within this span.
-                err = weight[r1:j] - weight_q[r1:j]
-                comp.addmm_(L[r1:j, r0:r1].T, err, alpha=1.0, beta=1.0)
-            rows = weight[r0:r1] + comp
-            tiles = rows.reshape(16, tiles_n, 16).permute(1, 0, 2).reshape(tiles_n, 256)
-            tiles = tiles[:, perm].contiguous()
-            if use_events:
-                ev0 = torch.cuda.Event(enable_timing=True)
-                ev0.record()
-            elif synchronize is not None:
-                synchronize()
-            t0 = time.perf_counter()
-            quant_w, quant_i = encode_tiles(tiles)
-            if use_events:
-                ev1 = torch.cuda.Event(enable_timing=True)
-                ev1.record()
-                events.append((ev0, ev1))
-            else:
-                if synchronize is not None:
-                    synchronize()
-                enc_s += time.perf_counter() - t0
-            calls += 1
-            if tuple(quant_w.shape) != (tiles_n, 256) or tuple(quant_i.shape) != (tiles_n, 256):
-                raise ValueError("encode_tiles must return two (tiles_n, 256) tensors, got "
-                                 f"{tuple(quant_w.shape)} / {tuple(quant_i.shape)}")
-            quant_w = quant_w.to(device=device, dtype=torch.float32)[:, inv_perm]
-            weight_q[r0:r1] = quant_w.reshape(tiles_n, 16, 16).permute(1, 0, 2).reshape(16, n)
-            encoded[r0 // 16] = _as_int16_states(quant_i.to(device=device))
-        # Span residual into the feedback of the spans above.
-        prod_cache.addmm_(L[i:j].T, weight[i:j] - weight_q[i:j], alpha=1.0, beta=1.0)
-
-    if events:
-        events[-1][1].synchronize()
-        enc_s = sum(a.elapsed_time(b) for a, b in events) / 1e3
-    check_finite = getattr(encode_tiles, "check_finite", None)
-    if check_finite is not None:
-        check_finite()
-    return LDLQResult(weight_q=weight_q, encoded=encoded, tiles_k=tiles_k, tiles_n=tiles_n,
-                      buf_size_k=buf_size_k, encoder_seconds=enc_s, encoder_calls=calls)
+def ldlq_lockstep(problems: Sequence[Tuple[torch.Tensor, torch.Tensor]],
+                  encode_tiles: TileEncoder, buf_size_k: int = DEFAULT_BUF_SIZE_K,
+                  synchronize: Callable[[], None] = None) -> List[LDLQResult]:
+    """:func:`ldlq` on several independent (weight, L) problems at once:
+    block b of every problem that has one goes through the same encoder
+    call, so a launch carries the sum of their tile rows instead of one
+    projection's. Each result equals its own :func:`ldlq` run (tiles are
+    encoded independently of their batch); ``encoder_seconds`` splits each
+    call's time by the problems' tile counts."""
+    if not problems:
+        return []
+    walks = [_Traversal(w, L, buf_size_k) for w, L in problems]
+    devices = {w.weight.device for w in walks}
+    if len(devices) != 1:
+        raise ValueError(f"all problems must be on one device, got {sorted(map(str, devices))}")
+    _run_lockstep(walks, encode_tiles, synchronize)
+    return [w.result() for w in walks]

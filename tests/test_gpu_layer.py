@@ -127,10 +127,16 @@ def test_quantize_decoder_layer_shared_arena(torch_mod):
     assert set(rep.module_results) == set(names)
     assert rep.tiles == sum(m.weight.numel() // 256 for m in layer.modules()
                             if isinstance(m, nn.Linear))
+    assert rep.extra["lockstep"] is True
+    # The reference's one-projection-at-a-time order gives the same states.
+    seq = quantize_decoder_layer(layer, hess, K=3, lockstep=False)
     for name, r in rep.module_results.items():
         assert np.isfinite(r.metrics.proxy_loss) and 0 < r.metrics.normalized_proxy_loss < 0.5
         k, n = r.original_shape
         assert r.encoded.shape == (k // 16, n // 16, 256)
+        assert torch_mod.equal(r.encoded, seq.module_results[name].encoded), name
+        assert torch_mod.equal(r.w_hat, seq.module_results[name].w_hat), name
+        assert r.metrics.encoder_calls == k // 16 and r.metrics.encoder_seconds > 0
 
 
 def test_ldlq_async_encoder_timing_and_nan(torch_mod):

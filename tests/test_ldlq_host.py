@@ -1,0 +1,75 @@
+"""Host logic of the LDLQ traversal (exl3_intel_arc_quantizer_amd/ldlq.py) on
+the CPU, with a deterministic grid quantiser standing in for the tile
+encoder: the torch traversal against the numpy oracle's (ldlq.py:163-309),
+and ldlq_lockstep against separate runs."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ldlq_ref
+
+
+def _grid_np(tiles):
+    return np.round(tiles * 4.0) / np.float32(4.0), np.zeros(tiles.shape, np.uint16)
+
+
+def _grid_torch(tiles):
+    q = torch.round(tiles * 4.0) / 4.0
+    # A state that depends on the tile values, so a misrouted block shows.
+    return q, (q * 4.0).to(torch.int16)
+
+
+def _problem(k, n, seed):
+    rng = np.random.default_rng(seed)
+    W = rng.standard_normal((k, n)).astype(np.float32)
+    X = rng.standard_normal((4 * k, k)).astype(np.float32)
+    H = (X.T @ X) / np.float32(X.shape[0]) + np.float32(0.05) * np.eye(k, dtype=np.float32)
+    L, _, _ = ldlq_ref.block_ldl(H.astype(np.float32))
+    return W, L
+
+
+def test_ldlq_matches_oracle_traversal():
+    from exl3_intel_arc_quantizer_amd.ldlq import ldlq
+    W, L = _problem(256, 128, 1)
+    got = ldlq(torch.from_numpy(W), torch.from_numpy(L), _grid_torch, buf_size_k=64)
+    want, _ = ldlq_ref.ldlq(W, L, _grid_np, buf=64)
+    np.testing.assert_allclose(got.weight_q.numpy(), want, rtol=0, atol=1e-6)
+    assert got.encoder_calls == 16 and got.encoded.shape == (16, 8, 256)
+
+
+def test_lockstep_equals_separate_runs():
+    from exl3_intel_arc_quantizer_amd.ldlq import ldlq, ldlq_lockstep
+    probs = [_problem(256, 128, 2), _problem(128, 256, 3), _problem(256, 384, 4)]
+    calls = []
+
+    def grid(tiles):
+        calls.append(tiles.shape[0])
+        return _grid_torch(tiles)
+
+    tp = [(torch.from_numpy(W), torch.from_numpy(L)) for W, L in probs]
+    together = ldlq_lockstep(tp, grid, buf_size_k=64)
+    # 16 steps; the 128-row problem stops after 8.
+    assert calls == [8 + 16 + 24] * 8 + [8 + 24] * 8
+    for (W, L), res in zip(tp, together):
+        alone = ldlq(W, L, _grid_torch, buf_size_k=64)
+        assert torch.equal(res.weight_q, alone.weight_q)
+        assert torch.equal(res.encoded, alone.encoded)
+        assert res.encoder_calls == alone.encoder_calls == W.shape[0] // 16
+
+
+def test_ldlq_rejects_bad_shapes_and_encoder_output():
+    from exl3_intel_arc_quantizer_amd.ldlq import ldlq, ldlq_lockstep
+    W, L = _problem(128, 128, 5)
+    Wt, Lt = torch.from_numpy(W), torch.from_numpy(L)
+    with pytest.raises(ValueError, match="multiple of 128"):
+        ldlq(Wt[:, :64], Lt, _grid_torch)
+    with pytest.raises(ValueError, match="L must be"):
+        ldlq(Wt, Lt[:64, :64], _grid_torch)
+    with pytest.raises(ValueError, match="buf_size_k"):
+        ldlq(Wt, Lt, _grid_torch, buf_size_k=24)
+    with pytest.raises(ValueError, match="encode_tiles must return"):
+        ldlq(Wt, Lt, lambda t: (t[:-1], t[:-1]))
+    assert ldlq_lockstep([], _grid_torch) == []
