@@ -27,6 +27,7 @@ _c_int, _c_i64, _c_vp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
 _SIGNATURES = {
     "exl3_last_error": (ctypes.c_char_p, []),
     "exl3_version": (ctypes.c_char_p, []),
+    "exl3_set_traceback_policy": (_c_int, [_c_int]),
     "exl3_decode_codebook": (_c_int, [_c_int, _c_vp, _c_vp]),
     "exl3_scratch_row_bytes": (_c_i64, [_c_int]),
     "exl3_scratch_edges_bytes": (_c_i64, [_c_int, _c_int, _c_i64]),
@@ -69,6 +70,19 @@ def load_library(path: Optional[Path] = None):
         _LIB = lib
     return lib
 
+
+
+TRACEBACK_POLICIES = {"auto": 0, "rows": 1, "stream": 2}
+
+
+def set_traceback_policy(policy: str) -> str:
+    """Choose the traceback kernel for later calls in this process: "auto"
+    (by batch size), "rows" (per-row tree loads) or "stream" (whole rows
+    streamed through LDS); results are identical. Returns the previous one."""
+    if policy not in TRACEBACK_POLICIES:
+        raise ValueError(f"policy must be one of {sorted(TRACEBACK_POLICIES)}, got {policy!r}")
+    prev = load_library().exl3_set_traceback_policy(TRACEBACK_POLICIES[policy])
+    return {v: k for k, v in TRACEBACK_POLICIES.items()}[prev]
 
 def last_error() -> str:
     return load_library().exl3_last_error().decode()

@@ -297,8 +297,8 @@ __device__ __forceinline__ u16x2 quad_min_u16x2(u16x2 v) {
 }
 
 // Cost-row forward pass (K = 1..7): minimum cost per edge, rows to HBM.
-// Thread `unit` owns edges jj*J .. jj*J + J - 1 of groups h0 .. h0 + G - 1,
-// in packed pairs (j, j + 1), and the Q = 2^K / P branches k = q*P + p of
+// Thread `unit` owns edges jj*J .. jj*J + J - 1 of G groups (one group, or
+// NV runs of GV consecutive groups when G > 1), in packed pairs (j, j + 1), and the Q = 2^K / P branches k = q*P + p of
 // lane p of its P-lane quad (interleaved, so the quad's LDS reads fall in
 // different banks). All edges of a group share the 2^K predecessor costs, so
 // each cost is broadcast to both halves of the FMA addend (op_sel) from a
@@ -330,7 +330,16 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
   const int p = tid % P;
   const int unit = tid / P;
   const int jj = unit % C::NJ;
-  const int h0 = (unit / C::NJ) * G;
+  // G > 1 (K = 1, 2): the thread's groups form NV runs of GV consecutive
+  // groups, one 16-byte vector of pair minima each, SV groups apart; lanes
+  // own adjacent runs, so each output vector store is contiguous over the
+  // wave (bank-conflict free) and each predecessor read is too.
+  constexpr int GV = G > 1 ? (8 >> K) : 1;
+  constexpr int NV = G / GV;
+  constexpr int SV = C::S / NV;
+  static_assert(G % GV == 0 && (G == 1 || GV % 2 == 0), "runs hold whole group pairs");
+  const int hbase = (unit / C::NJ) * GV;
+  auto grp = [&](int g) { return (g / GV) * SV + hbase + (g % GV); };
 
   f16x2 cbv[G][JP][C::Q];
 #pragma unroll
@@ -340,7 +349,7 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
 #pragma unroll
       for (int q = 0; q < C::Q; ++q) {
         const uint32_t s_lo = ((uint32_t)(q * P + p) << C::KR) |
-                              ((uint32_t)(h0 + g) << K) | (uint32_t)(jj * J + 2 * jp);
+                              ((uint32_t)grp(g) << K) | (uint32_t)(jj * J + 2 * jp);
         f16x2 v;
         v.x = decode_state(CB, s_lo);
         v.y = decode_state(CB, s_lo + 1u);
@@ -366,16 +375,17 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
     for (int q = 0; q < C::Q; q += 2) {
       const int k = q * P + p;
       // cw[b][g2]: predecessor costs of branch k (b = 0) and k + P (b = 1)
-      // for groups h0 + 2 g2 (low half) and h0 + 2 g2 + 1 (high half).
+      // for groups grp(2 g2) (low half) and grp(2 g2) + 1 (high half).
       uint32_t cw[2][(G + 1) / 2];
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
-        const uint16_t* src = cin + (k + b * P) * SP + h0;
+        const uint16_t* src = cin + (k + b * P) * SP;
         if constexpr (G == 1) {
-          cw[b][0] = src[0];
+          cw[b][0] = src[grp(0)];
         } else {
 #pragma unroll
-          for (int g2 = 0; g2 < G / 2; ++g2) cw[b][g2] = reinterpret_cast<const uint32_t*>(src)[g2];
+          for (int g2 = 0; g2 < G / 2; ++g2)
+            cw[b][g2] = *reinterpret_cast<const uint32_t*>(src + grp(2 * g2));
         }
       }
 #pragma unroll
@@ -404,7 +414,7 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
 #pragma unroll
       for (int jp = 0; jp < JP; ++jp) {
         const u16x2 v = quad_min_u16x2<P>(__builtin_bit_cast(u16x2, m[g][jp]));
-        const int e = ((h0 + g) << K) | (jj * J + 2 * jp);
+        const int e = (grp(g) << K) | (jj * J + 2 * jp);
         if (P == 1 || p == 0) cout[lds_pos<KS, PAD>(e) >> 1] = __builtin_bit_cast(uint32_t, v);
       }
     __syncthreads();
@@ -566,7 +576,40 @@ __global__ void __launch_bounds__(256) traceback_bp_kernel(TbArgs a) {
 // reduced inside a lane and a lane's leaves are one aligned vector load.
 // Once a level has reduced every register bit, the registers of a lane hold
 // copies of one value and the remaining digits reduce across lanes with
-// __shfl_xor. Trees with fewer than 64 leaves are replicated over the wave.
+// xor_min (DPP / permlane swaps). Trees with fewer than 64 leaves are
+// replicated over the wave.
+
+// min(v, v of lane ^ mask) for mask = 1 .. 32 without the LDS crossbar:
+// DPP quad_perm (1, 2), quad reversal then row_half_mirror (4: i ^ 3 ^ 7),
+// row_ror:8 (8), and gfx950's v_permlane16_swap / v_permlane32_swap (16,
+// 32: the swapped pair holds each lane's value and its partner's). mask
+// must fold to a constant; every lane of the wave must be active.
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v, int ctrl) {
+  switch (ctrl) {
+    case 0xB1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    case 0x4E: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+    case 0x1B: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x1B, 0xF, 0xF, false);
+    case 0x141: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);
+    default: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+  }
+}
+
+__device__ __forceinline__ uint32_t xor_min(uint32_t v, int mask) {
+  switch (mask) {
+    case 1: return umin(v, dpp_mov(v, 0xB1));
+    case 2: return umin(v, dpp_mov(v, 0x4E));
+    case 4: return umin(v, dpp_mov(dpp_mov(v, 0x1B), 0x141));
+    case 8: return umin(v, dpp_mov(v, 0x128));
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+      return umin(r[0], r[1]);
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+      return umin(r[0], r[1]);
+    }
+  }
+}
 
 template <int N>
 struct U16Vec {
@@ -669,7 +712,7 @@ __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ leaf,
     if (hi > RLOG) {
 #pragma unroll
       for (int b = (lo > RLOG ? lo : RLOG); b < (hi < NLOG ? hi : NLOG); ++b)
-        v[0] = umin(v[0], (uint32_t)__shfl_xor((int)v[0], 1 << (b - RLOG), 64));
+        v[0] = xor_min(v[0], 1 << (b - RLOG));
 #pragma unroll
       for (int r = 1; r < R; ++r) v[r] = v[0];
     }
@@ -688,7 +731,7 @@ __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ leaf,
   }
 #pragma unroll
   for (int b = (K * D > RLOG ? K * D : RLOG); b < NLOG; ++b)
-    key = umin(key, (uint32_t)__shfl_xor((int)key, 1 << (b - RLOG), 64));
+    key = xor_min(key, 1 << (b - RLOG));
   return key & 0xFFFFu;
 }
 
@@ -768,6 +811,159 @@ __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
     if (!a.write && ri == 0) break;
   }
   if (!a.write && lane == 0) a.end_out[(int64_t)t * a.end_stride] = (int32_t)edge;
+}
+
+// Streamed cost-row traceback for small batches. The traceback above is
+// bound by one dependent HBM load per stored row and tile; with few tiles
+// in flight that latency is the whole kernel. Here one workgroup per tile
+// streams every stored row it will visit into a two-slot LDS ring ahead of
+// the walk (the rows are known in advance, only the tree inside a row
+// depends on the path): wave 0 walks exactly as traceback_rows_kernel,
+// reading its trees from the ring; NG loader groups of W waves take rows in
+// turn (row j belongs to group j % NG), so a row's load has NG rows of walk
+// time to arrive while every group keeps one row in statically indexed
+// registers. One workgroup barrier per stored row, LDS-only fences so loads
+// stay in flight across it. Reads every row whole (E x 2 bytes instead of
+// one tree), so it pays off only while HBM bandwidth is idle.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int K>
+struct StreamShape {
+  static constexpr int W = (K == 1 || K == 2) ? 4 : (K <= 4 ? 2 : 1);  // waves per group
+  static constexpr int NG = (K == 1) ? 1 : (K == 2 ? 2 : (K <= 5 ? 4 : 8));
+  static constexpr int THREADS = 64 * (1 + W * NG);
+};
+
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int K, int CB>
+__global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kernel(TbArgs a) {
+  constexpr int KR = 16 - K;
+  constexpr int STRIDE = exl3::row_stride(K);
+  constexpr int MAXLEAF = 1 << (K * STRIDE);
+  constexpr int RV = 2 * (65536 >> K) / 16;  // 16-byte vectors per row
+  constexpr int W = StreamShape<K>::W, NG = StreamShape<K>::NG;
+  constexpr int NLT = 64 * W;                // threads per loader group
+  constexpr int V = RV / NLT;
+  static_assert(RV % NLT == 0 && V >= 1, "rows split evenly over a loader group");
+  __shared__ u32x4 s_ring[2][RV];
+  __shared__ __attribute__((aligned(16))) uint16_t s_leaf[MAXLEAF];
+  __shared__ uint16_t s_wbits[256];
+  __shared__ uint16_t s_oidx[256];
+  __shared__ float s_ow[256];
+  const int t = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int L = a.L, roll = a.roll;
+  const uint8_t* blk = a.scratch + (int64_t)t * a.tile_stride;
+  const uint8_t* hdr = blk + a.hdr_offset;
+  const int row_bytes = a.lay.row_bytes;
+  const int pre = reinterpret_cast<const int32_t*>(hdr)[exl3::HDR_PRE_STATE];
+  const uint16_t* wsrc = reinterpret_cast<const uint16_t*>(hdr + exl3::HDR_W_BYTES);
+  for (int r = threadIdx.x; r < L; r += StreamShape<K>::THREADS) s_wbits[r] = wsrc[r];
+
+  // Steps L-1 .. i_stop are walked; steps >= 1 read the stored row
+  // r0(i) = (i - 1) - (i - 1) % STRIDE, rows top, top - STRIDE, ..., r_last.
+  const int i_stop = a.write ? 0 : (L - roll) % L;
+  const int last_i = i_stop > 1 ? i_stop : 1;
+  const int top = (L - 2) - (L - 2) % STRIDE;
+  const int r_last = (last_i - 1) - (last_i - 1) % STRIDE;
+  const int NR = (top - r_last) / STRIDE + 1;
+  auto row_src = [&](int q) {
+    return reinterpret_cast<const u32x4*>(blk + (int64_t)((top - q * STRIDE) / STRIDE) * row_bytes);
+  };
+
+  const int g = (wave - 1) / W;              // loader group (wave >= 1)
+  const int lt = threadIdx.x - 64 - g * NLT;
+  u32x4 buf[V];  // native vectors: registers, not scratch
+  if (wave > 0) {
+    if (g < NR) {
+      const u32x4* src = row_src(g);
+#pragma unroll
+      for (int v = 0; v < V; ++v) buf[v] = src[lt + v * NLT];
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) s_ring[0][lt + v * NLT] = buf[v];
+      if (NG < NR) {
+        const u32x4* src = row_src(NG);
+#pragma unroll
+        for (int v = 0; v < V; ++v) buf[v] = src[lt + v * NLT];
+      }
+    }
+  }
+  lds_barrier();
+
+  const uint16_t* wbits = s_wbits;
+  uint32_t edge = (uint32_t)a.start[(int64_t)t * a.start_stride] & ((65536u >> K) - 1u);
+  int i = L - 1;
+  int base = 0;
+  for (int q = 0; q < NR; ++q) {
+    if (wave == 0) {
+      const uint16_t* row = reinterpret_cast<const uint16_t*>(s_ring[q & 1]);
+      const int r = top - q * STRIDE;
+      bool fresh = true;
+      while (i >= last_i && (i - 1) - (i - 1) % STRIDE == r) {
+        int ri = i + roll;
+        if (ri >= L) ri -= L;
+        const int d = (i - 1) % STRIDE;
+        if (fresh) {
+          tb_load_dispatch<K, 0>(d, row, edge, s_leaf, lane);
+          __builtin_amdgcn_wave_barrier();
+          base = 0;
+          fresh = false;
+        }
+        const uint32_t k = tb_dispatch<K, CB, 0>(d, s_leaf + base, edge, wbits, ri, L, lane, pre);
+        base += (int)k << (K * d);
+        const uint32_t sigma = (k << KR) | edge;
+        if (a.write && lane == 0) {
+          s_oidx[ri] = (uint16_t)sigma;
+          s_ow[ri] = (float)decode_state(CB, sigma);
+        }
+        edge = sigma >> K;
+        --i;
+      }
+      __builtin_amdgcn_wave_barrier();  // this tree's readers before the next load
+    } else {
+      const int j = q + 1;  // the row to place in the ring this iteration
+      if (j < NR && j % NG == g) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) s_ring[j & 1][lt + v * NLT] = buf[v];
+        if (j + NG < NR) {
+          const u32x4* src = row_src(j + NG);
+#pragma unroll
+          for (int v = 0; v < V; ++v) buf[v] = src[lt + v * NLT];
+        }
+      }
+    }
+    lds_barrier();
+  }
+
+  if (wave != 0) return;
+  if (i_stop == 0) {  // step 0: predecessors from the start constraint
+    int ri = roll;
+    if (ri >= L) ri -= L;
+    const uint32_t k = tb_branch<K, CB, 0, true>(nullptr, edge, wbits, ri, L, lane, pre);
+    const uint32_t sigma = (k << KR) | edge;
+    if (a.write && lane == 0) {
+      s_oidx[ri] = (uint16_t)sigma;
+      s_ow[ri] = (float)decode_state(CB, sigma);
+    }
+    edge = sigma >> K;
+  }
+  if (a.write) {
+    __builtin_amdgcn_wave_barrier();
+    for (int r = lane; r < L; r += 64) {
+      a.out_idx[(int64_t)t * L + r] = (int16_t)s_oidx[r];
+      a.out_w[(int64_t)t * L + r] = s_ow[r];
+    }
+  } else if (lane == 0) {
+    a.end_out[(int64_t)t * a.end_stride] = (int32_t)edge;
+  }
 }
 
 // ---------------------------------------------------------- prepare/finalize
@@ -975,8 +1171,33 @@ static FwdArgs forward_args(const float* in, int n, int K, int cb, int L, uint8_
   return a;
 }
 
+// Traceback kernel choice: 0 = by batch size, 1 = per-row tree loads
+// (traceback_rows_kernel), 2 = streamed rows (traceback_stream_kernel).
+static int g_traceback_policy = 0;
+
+// The streamed traceback reads each visited row whole: it wins while that
+// traffic (tiles x rows x row bytes) stays small next to what the
+// latency-bound walk costs, i.e. for the few-hundred-tile launches of the
+// LDLQ block loop.
+static bool use_stream_traceback(const TbArgs& a) {
+  if (g_traceback_policy == 1) return false;
+  if (g_traceback_policy == 2) return true;
+  const int64_t walk_rows = (int64_t)(a.L - 1) / exl3::row_stride(a.lay.K) + 1;
+  const int64_t bytes = (int64_t)a.n * walk_rows * a.lay.row_bytes;
+  return bytes <= ((int64_t)384 << 20);
+}
+
 template <int K>
 static void launch_traceback_rows(const TbArgs& a, hipStream_t st) {
+  if (use_stream_traceback(a)) {
+    const dim3 blk(StreamShape<K>::THREADS);
+    switch (a.cb) {
+      case 0: hipLaunchKernelGGL((traceback_stream_kernel<K, 0>), dim3(a.n), blk, 0, st, a); break;
+      case 1: hipLaunchKernelGGL((traceback_stream_kernel<K, 1>), dim3(a.n), blk, 0, st, a); break;
+      default: hipLaunchKernelGGL((traceback_stream_kernel<K, 2>), dim3(a.n), blk, 0, st, a); break;
+    }
+    return;
+  }
   switch (a.cb) {
     case 0: hipLaunchKernelGGL((traceback_rows_kernel<K, 0>), dim3(a.n), dim3(64), 0, st, a); break;
     case 1: hipLaunchKernelGGL((traceback_rows_kernel<K, 1>), dim3(a.n), dim3(64), 0, st, a); break;
@@ -1025,6 +1246,14 @@ extern "C" {
 const char* exl3_last_error(void) { return g_last_error.c_str(); }
 
 const char* exl3_version(void) { return EXL3_VERSION; }
+
+int exl3_set_traceback_policy(int policy) {
+  if (policy < 0 || policy > 2)
+    return set_error("traceback policy must be 0, 1 or 2, got %d", policy), -1;
+  const int previous = g_traceback_policy;
+  g_traceback_policy = policy;
+  return previous;
+}
 
 int exl3_decode_codebook(int cb, uint16_t* lut, void* stream) {
   if (cb < 0 || cb > 2) return set_error("cb must be 0, 1, or 2, got %d", cb);

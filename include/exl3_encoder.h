@@ -51,6 +51,13 @@ const char* exl3_last_error(void);
 /* Library version string. */
 const char* exl3_version(void);
 
+/* Traceback kernel choice for every later call in this process (no
+ * counterpart in the reference, whose traceback has one form): 0 = by
+ * batch size (default), 1 = per-row tree loads, 2 = whole rows streamed
+ * through LDS. Both kernels give identical results. Returns the previous
+ * policy, or -1 for a value outside 0..2. */
+int exl3_set_traceback_policy(int policy);
+
 /* Replaces decode_codebook (quantize_xpu.cpp:105-110,
  * quantize_kernels.sycl:594-601): fp16 bits of all 65536 states. */
 int exl3_decode_codebook(int cb, uint16_t* lut, void* stream);

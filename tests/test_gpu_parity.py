@@ -308,6 +308,36 @@ def test_tile_encoder_nan_rejection(torch_mod):
         enc.encoder.arena.release()
 
 
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7])
+def test_traceback_kernels_agree(K):
+    """The two cost-row tracebacks (per-row tree loads, whole rows streamed
+    through LDS) give the oracle's states in both passes, through the fused
+    entry point and the split forward / backward entry points."""
+    from exl3_intel_arc_quantizer_amd import _native
+    rng = np.random.default_rng(600 + K)
+    tiles = rng.normal(0.0, 1.0, size=(12, 256)).astype(np.float32)
+    tiles[3] *= 4.0
+    tiles[7, ::5] = 0.0
+    ref = c_oracle.encode_tiles(tiles, K=K, cb=2, pre_permute=True)
+    prev = _native.set_traceback_policy("auto")
+    try:
+        for policy in ("rows", "stream"):
+            _native.set_traceback_policy(policy)
+            for mode in ("gpu_resident", "gpu_resident_split"):
+                print(f"K={K} traceback={policy} mode={mode}", flush=True)
+                enc = _encoder(K=K, cb=2)
+                try:
+                    bd = enc.encode_batch_detailed(tiles, requested_b=12, traceback_mode=mode)
+                finally:
+                    enc.arena.release()
+                np.testing.assert_array_equal(bd.output_indices, ref.output_indices,
+                                              err_msg=f"{policy} {mode}")
+                np.testing.assert_array_equal(bd.end_states, ref.end_state,
+                                              err_msg=f"{policy} {mode}")
+    finally:
+        _native.set_traceback_policy(prev)
+
+
 def test_traceback_modes_and_variants_agree():
     """tests/test_xpu_quantizer.py:299-330."""
     rng = np.random.default_rng(909)

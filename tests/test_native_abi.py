@@ -103,3 +103,15 @@ def test_forward_and_backward_reject_bad_arguments():
     assert lib.exl3_pack_trellis(None, None, 0, 2, None) != 0
     assert lib.exl3_prepare_tiles(None, None, 1, 160, 1, None, None) != 0
     assert "pre_permute" in lib.exl3_last_error().decode()
+
+
+def test_traceback_policy_switch():
+    """exl3_set_traceback_policy only records the choice (no GPU work)."""
+    lib = _native.load_library()
+    assert lib.exl3_set_traceback_policy(3) == -1
+    assert b"policy" in lib.exl3_last_error()
+    assert _native.set_traceback_policy("rows") == "auto"
+    assert _native.set_traceback_policy("stream") == "rows"
+    assert _native.set_traceback_policy("auto") == "stream"
+    with pytest.raises(ValueError):
+        _native.set_traceback_policy("fast")
