@@ -42,6 +42,7 @@ _SIGNATURES = {
     "exl3_finalize_tiles": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                      _c_i64, _c_int, _c_int, _c_int, _c_vp]),
     "exl3_pack_trellis": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
+    "exl3_unpack_trellis": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
     "exl3_probe_hfma": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
 }
 
@@ -410,6 +411,20 @@ class QuantizeExtension:
         with torch.cuda.device(dev):
             _check(self.lib.exl3_pack_trellis(states.data_ptr(), packed.data_ptr(), n, K,
                                               _stream(dev)), "pack_trellis")
+
+    def unpack_trellis(self, packed, states, K: int) -> None:
+        """Packed (n, 16*K) int16 tiles back to (n, 256) int16 states."""
+        torch = _torch()
+        dev = _check_device_tensor(packed, "packed", torch.int16, 2)
+        _check_device_tensor(states, "states", torch.int16, 2)
+        n = packed.size(0)
+        if not 1 <= K <= 8 or packed.size(1) != 16 * K or tuple(states.shape) != (n, 256):
+            raise RuntimeError("unpack_trellis expects (n, 16*K) words and (n, 256) states")
+        if states.device != packed.device:
+            raise RuntimeError("states must be on the same GPU device as packed")
+        with torch.cuda.device(dev):
+            _check(self.lib.exl3_unpack_trellis(packed.data_ptr(), states.data_ptr(), n, K,
+                                                _stream(dev)), "unpack_trellis")
 
     def probe_hfma(self, dh, cost, out, mode: int) -> None:
         """exl3_quant/xpu_probe.py ``probe_hfma`` (mode 0: fused, 1: two roundings)."""

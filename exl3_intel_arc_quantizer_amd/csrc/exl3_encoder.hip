@@ -1088,6 +1088,25 @@ __global__ void pack_kernel(const int16_t* __restrict__ states, uint16_t* __rest
   }
 }
 
+// Inverse of pack_kernel (trellis_format.py:181-213): state t of a tile is
+// the 16-bit window of the tile's MSB-first bitstream ending at bit
+// (t + 1) K, circular. Stream word w is storage word w ^ 1 (swap16), so the
+// window is two neighbouring words shifted; one thread per state.
+__global__ void unpack_kernel(const uint16_t* __restrict__ packed, int16_t* __restrict__ states,
+                              int64_t n, int K) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n * 256) return;
+  const int64_t tile = gid >> 8;
+  const int t = (int)(gid & 255);
+  const int nbits = 256 * K, words = 16 * K;
+  const int p0 = ((t + 1) * K - 16 + nbits) % nbits;
+  const int w0 = p0 >> 4, off = p0 & 15;
+  const uint16_t* src = packed + tile * words;
+  const uint32_t hi = src[w0 ^ 1];
+  const uint32_t lo = src[((w0 + 1) % words) ^ 1];
+  states[gid] = (int16_t)(uint16_t)((((hi << 16) | lo) >> (16 - off)) & 0xFFFFu);
+}
+
 __global__ void probe_hfma_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ c,
                                   uint16_t* __restrict__ out, int64_t n, int mode) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1407,6 +1426,16 @@ int exl3_pack_trellis(const int16_t* states, uint16_t* packed, int64_t n, int K,
   hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((total + block - 1) / block)), dim3(block), 0,
                      as_stream(stream), states, packed, n, K);
   return check_launch("pack_trellis");
+}
+
+int exl3_unpack_trellis(const uint16_t* packed, int16_t* states, int64_t n, int K, void* stream) {
+  if (n <= 0 || K < 1 || K > 8) return set_error("bad unpack arguments");
+  if (!packed || !states) return set_error("NULL buffer");
+  const int64_t total = n * 256;
+  const int block = 256;
+  hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)((total + block - 1) / block)), dim3(block), 0,
+                     as_stream(stream), packed, states, n, K);
+  return check_launch("unpack_trellis");
 }
 
 int exl3_probe_hfma(const uint16_t* a, const uint16_t* c, uint16_t* out, int64_t n, int mode,

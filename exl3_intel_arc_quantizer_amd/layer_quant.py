@@ -29,6 +29,7 @@ from .hadamard import HAD_DIM, blockwise_preapply_had_l_, blockwise_preapply_had
     weight_from_quantized
 from .ldlq import (DEFAULT_BLOCK_SIZE, DEFAULT_BUF_SIZE_K, BlockLDLResult, LDLQResult,
                    block_ldl, ldlq, ldlq_lockstep)
+from .gss import g_scale_fn_from_encoder
 from .regularize import RegularizeResult, regularize
 from .tile_encoder import TileEncoder, make_xpu_tile_encoder
 from .trellis_format import CB_MUL1
@@ -175,10 +176,10 @@ class _PreparedModule:
 
 
 def _prepare_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int,
-                    tile_encoder: Optional[TileEncoder], skip_g_scale: bool,
+                    tile_encoder: TileEncoder, skip_g_scale: bool,
                     block_size: int) -> _PreparedModule:
-    """Shape checks, regularisation, Hessian rotation and block LDL
-    (layer_quant.py:130-214)."""
+    """Shape checks, regularisation (with the global-scale search unless
+    ``skip_g_scale``), Hessian rotation and block LDL (layer_quant.py:130-214)."""
     t0 = time.time()
     if weight.dim() != 2:
         raise ValueError(f"weight must be 2D, got shape {tuple(weight.shape)}")
@@ -193,16 +194,16 @@ def _prepare_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int,
     else:
         raise ValueError(f"Weight shape {tuple(weight.shape)} does not match Hessian dim {k_dim}")
     k, n = W.shape
-    enc_k = getattr(tile_encoder, "K", None) if tile_encoder is not None else None
+    enc_k = getattr(tile_encoder, "K", None)
     if enc_k is not None and enc_k != K:
         raise ValueError(f"Tile encoder K={enc_k} does not match the requested K={K}.")
-    if not skip_g_scale:
-        raise ValueError("the global-scale search (skip_g_scale=False) is not part of this build")
+    # Global scale from the same encoder (layer_quant.py:197-203).
+    g_scale_fn = None if skip_g_scale else g_scale_fn_from_encoder(tile_encoder)
 
     su = torch.ones((k, 1), dtype=torch.float32, device=device)
     sv = torch.ones((1, n), dtype=torch.float32, device=device)
-    reg = regularize(weight=W, su=su, sv=sv, H_diag=H.diagonal(), skip_g_scale=True,
-                     had_dim=HAD_DIM)
+    reg = regularize(weight=W, su=su, sv=sv, H_diag=H.diagonal(), skip_g_scale=skip_g_scale,
+                     g_scale_fn=g_scale_fn, had_dim=HAD_DIM)
 
     H_work = H.to(torch.float32).clone()
     blockwise_preapply_had_l_(H_work, HAD_DIM)
@@ -244,9 +245,11 @@ def quantize_linear_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: 
     """Quantise one linear weight with LDLQ (layer_quant.py:130-265). The
     weight is (out, in) as in ``nn.Linear`` or already (in, out) = (k, n);
     ``H`` is (in, in). Runs on the device of ``H``, which must be a GPU."""
-    pm = _prepare_module(name, weight, H, K, tile_encoder, skip_g_scale, block_size)
+    if H.device.type != "cuda":
+        raise ValueError("quantize_linear_module runs on the GPU; move H to a cuda device")
     if tile_encoder is None:
         tile_encoder = make_xpu_tile_encoder(K=K, device_index=H.device.index or 0)
+    pm = _prepare_module(name, weight, H, K, tile_encoder, skip_g_scale, block_size)
     t0 = time.time()
     lq = ldlq(weight=pm.reg.weight, L=pm.ldl.transformed, encode_tiles=tile_encoder,
               buf_size_k=buf_size_k)

@@ -131,6 +131,11 @@ int exl3_finalize_tiles(const float* x, const float* raw, const float* out_w,
  * 256 int16 states: packed is uint16 [n][16K]. */
 int exl3_pack_trellis(const int16_t* states, uint16_t* packed, int64_t n, int K, void* stream);
 
+/* decode_states (trellis_format.py:181-213) for n packed tiles, the read-back
+ * of unpack_module_trellis (serialization.py:65-84): states[t][i] is the
+ * 16-bit window of tile t's bitstream ending at bit (i + 1) K, circular. */
+int exl3_unpack_trellis(const uint16_t* packed, int16_t* states, int64_t n, int K, void* stream);
+
 /* fp16 fused multiply-add probe (xpu_probe.py:153-272): out[i] =
  * fp16(a[i]*a[i] + c[i]) with one rounding (mode 0) or the two-rounding
  * expression fp16(fp16(a*a) + c) (mode 1). */
