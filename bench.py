@@ -307,6 +307,34 @@ def run_decoder_config(torch, K=4, cpu_tiles_per_s=None, lockstep=True):
     return out
 
 
+def run_host_api(torch, tiles, K=4, steps=5):
+    """configs[1] through the reference's host-array API
+    (XPUTrellisEncoder.encode_batch_detailed, xpu_quantizer.py:707-909):
+    numpy tiles in, numpy states / packed words / path costs / distortions
+    out, so PCIe transfers and host result assembly are inside the timing
+    (per-tile EncodingResult objects skipped: build_results=False)."""
+    from exl3_intel_arc_quantizer_amd.gpu_quantizer import XPUTrellisEncoder
+    enc = XPUTrellisEncoder(K=K, cb=2)
+    try:
+        enc.encode_batch_detailed(tiles, pre_permute=True, build_results=False)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            bd = enc.encode_batch_detailed(tiles, pre_permute=True, build_results=False)
+        dt = (time.perf_counter() - t0) / steps
+    finally:
+        enc.arena.release()
+    return {"metric": "configs[1] tiles/s through the host-array API (PCIe and host assembly "
+                      "included), K=4, 1 MI355X",
+            "value": round(tiles.shape[0] / dt, 1), "unit": "tiles/s", "higher_is_better": True,
+            "n_gpus": 1, "steps": steps, "ms_per_step": round(dt * 1e3, 3), "dtype": "fp16",
+            "data": "synthetic", "config": {"workload": "configs[1]", "K": K,
+                                            "tiles": int(tiles.shape[0])},
+            "breakdown_ms": {k: round(v * 1e3, 3) for k, v in (
+                ("transfer", bd.transfer_seconds), ("search", bd.search_seconds),
+                ("traceback", bd.traceback_seconds), ("post_process", bd.postprocess_seconds),
+                ("total", bd.total_seconds))}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -323,6 +351,8 @@ def main() -> int:
                     help="configs[3]: LDLQ-driven 4096x4096 layer (prints its own JSON line)")
     ap.add_argument("--decoder", action="store_true",
                     help="configs[4]: 9B-class decoder layer conversion (its own JSON line)")
+    ap.add_argument("--host-api", action="store_true",
+                    help="configs[1] through encode_batch_detailed (numpy in/out; PCIe-inclusive)")
     ap.add_argument("--sequential", action="store_true",
                     help="with --decoder: one projection at a time (the reference's order)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -339,6 +369,10 @@ def main() -> int:
     k_list = [int(k) for k in args.k_list.split(",")]
     head = k_list[0]
     cpu = cpu_np = None
+    if args.host_api:
+        import torch
+        print(json.dumps(run_host_api(torch, tiles)), flush=True)
+        return 0
     if args.layer or args.decoder:
         import torch
         if args.decoder and not args.no_cpu_baseline:

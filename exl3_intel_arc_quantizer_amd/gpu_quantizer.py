@@ -226,7 +226,7 @@ class ScratchArena:
                 torch.cuda.synchronize(self.device_index)
             self.reuses += 1
             snap = capture_snapshot(self.device_index)
-            out_bytes = int(torch.cuda.memory_allocated(self.device_index))
+            out_bytes = snap.device_allocated_bytes
             self._log("reuse", k, tile_len, target_b, target_b, self.resident_bytes,
                       distinct_staging_bytes, out_bytes,
                       self.policy.usable_bytes(snap, out_bytes + distinct_staging_bytes), snap)
@@ -355,6 +355,7 @@ class XPUTrellisEncoder:
         self.force_global_costs = force_global_costs
         self.wave_cap_override = wave_cap_override
         self.arena = arena or ScratchArena(device_index=device_index)
+        self._pinned_bufs = {}
         self._lut = None
         if self.L == 256:
             self.perm = tensor_core_perm()
@@ -381,6 +382,18 @@ class XPUTrellisEncoder:
     @property
     def device(self) -> str:
         return f"cuda:{self.device_index}"
+
+    def _pinned(self, key: str, nbytes: int):
+        """A page-locked host byte buffer of at least ``nbytes``, kept per
+        encoder and reused by later calls (each call synchronises before it
+        returns, so no copy is in flight when the buffer is refilled)."""
+        import torch
+
+        buf = self._pinned_bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, pin_memory=True)
+            self._pinned_bufs[key] = buf
+        return buf[:nbytes]
 
     def encode_tile(self, tile: np.ndarray, pre_permute: bool = True,
                     traceback_mode: str = "gpu_resident") -> EncodingResult:
@@ -546,13 +559,16 @@ class XPUTrellisEncoder:
         arr = np.asarray(tiles, dtype=np.float32)
         n, width = self._flatten(arr.shape)
         self._check_mode(n, width, pre_permute, traceback_mode)
-        flat = np.ascontiguousarray(arr.reshape(n, width))
+        flat = arr.reshape(n, width)
         if np.isnan(flat).any():
             raise ValueError("NaN tile values are not supported (see module docstring)")
 
         t_total0 = time.perf_counter()
         t0 = time.perf_counter()
-        raw_dev = torch.from_numpy(flat).to(self.device)
+        # Through a reused pinned buffer: DMA-speed copies both ways.
+        staging = self._pinned("in", n * width * 4).view(torch.float32).view(n, width)
+        staging.numpy()[...] = flat
+        raw_dev = staging.to(self.device, non_blocking=True)
         torch.cuda.synchronize(self.device_index)
         t_transfer = time.perf_counter() - t0
 
@@ -560,13 +576,27 @@ class XPUTrellisEncoder:
                                  traceback_mode=traceback_mode, finalize=True,
                                  allocator_hook=allocator_hook)
         tx = time.perf_counter()
-        idx = enc["indices"].cpu().numpy().view(np.uint16)
-        rec_perm = enc["reconstructed_perm"].cpu().numpy().astype(np.float16)
-        rec = enc["reconstructed"].cpu().numpy().view(np.float16)
-        packed = (enc["packed"].cpu().numpy().view(np.uint16) if enc["packed"] is not None
+        outs = [("idx", enc["indices"]), ("rec_perm", enc["reconstructed_perm"].to(torch.float16)),
+                ("rec", enc["reconstructed"]), ("path_cost", enc["path_cost"]),
+                ("distortion", enc["distortion"])]
+        if enc["packed"] is not None:
+            outs.append(("packed", enc["packed"]))
+        sizes = [-(-t.numel() * t.element_size() // 16) * 16 for _, t in outs]
+        host_buf = self._pinned("out", sum(sizes))
+        host, off = {}, 0
+        for (name, t), size in zip(outs, sizes):
+            view = host_buf[off:off + t.numel() * t.element_size()].view(t.dtype).view(t.shape)
+            view.copy_(t, non_blocking=True)
+            host[name] = view
+            off += size
+        torch.cuda.synchronize(self.device_index)
+        idx = host["idx"].numpy().view(np.uint16).copy()
+        rec_perm = host["rec_perm"].numpy().copy()
+        rec = host["rec"].numpy().view(np.float16).copy()
+        packed = (host["packed"].numpy().view(np.uint16).copy() if "packed" in host
                   else np.zeros((n, 0), dtype=np.uint16))
-        path_cost = enc["path_cost"].cpu().numpy()
-        distortion = enc["distortion"].cpu().numpy()
+        path_cost = host["path_cost"].numpy().copy()
+        distortion = host["distortion"].numpy().copy()
         t_transfer += time.perf_counter() - tx
         total_seconds = time.perf_counter() - t_total0
         del raw_dev, enc["x"]

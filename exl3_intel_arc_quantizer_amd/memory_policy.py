@@ -123,8 +123,11 @@ def capture_snapshot(device_index: int = 0, meminfo_path: Optional[str] = None) 
 
         if torch.cuda.is_available():
             free, total = (int(v) for v in torch.cuda.mem_get_info(device_index))
-            allocated = int(torch.cuda.memory_allocated(device_index))
-            reserved = int(torch.cuda.memory_reserved(device_index))
+            # One read of the allocator's nested counters (memory_allocated /
+            # memory_reserved each rebuild the flattened statistics dict).
+            stats = torch.cuda.memory_stats_as_nested_dict(device_index)
+            allocated = int(stats.get("allocated_bytes", {}).get("all", {}).get("current", 0))
+            reserved = int(stats.get("reserved_bytes", {}).get("all", {}).get("current", 0))
             gpu_available = True
     except Exception:  # pragma: no cover - broken driver / CPU-only host
         gpu_available = False
