@@ -209,7 +209,8 @@ def run_layer_config(torch, K=4):
     """one 4096x4096 linear layer, W ~ N(0, 0.02^2) (seed 3),
     Hessian X^T X / 8192 from bf16 activations [8192, 4096] (seed 4, 5 % of
     channels x10), damped 1 %, Hadamard-rotated inside the driver, LDLQ with
-    buf_size_k = 128 at K = 4 (256 encoder calls of 256 tiles)."""
+    buf_size_k = 128 at K = 4 (256 encoder calls of 256 tiles). The reported
+    wall time is the median of three runs after a 256x256 warm-up layer."""
     from exl3_intel_arc_quantizer_amd.layer_quant import (hessian_from_activations,
                                                           quantize_linear_module)
     W = torch.from_numpy((np.random.default_rng(3).standard_normal((4096, 4096),
@@ -220,10 +221,16 @@ def run_layer_config(torch, K=4):
     del X
     quantize_linear_module("warmup", W[:256, :256].cuda(), H[:256, :256].contiguous(), K=K)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    res = quantize_linear_module("layer", W.cuda(), H, K=K)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    # A 0.2 s run is sensitive to clock ramp and host jitter: time three
+    # full-size runs and report the median one.
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        res = quantize_linear_module("layer", W.cuda(), H, K=K)
+        torch.cuda.synchronize()
+        runs.append((time.perf_counter() - t0, res))
+    runs.sort(key=lambda r: r[0])
+    wall, res = runs[1]
     m = res.metrics
     tiles = 4096 * 4096 // 256
     return {"metric": "LDLQ-driven 4096x4096 layer, K=4, 1 MI355X: wall time", "value": round(wall, 3),
@@ -231,6 +238,7 @@ def run_layer_config(torch, K=4):
             "config": {"workload": "configs[3]", "K": K, "buf_size_k": 128, "tiles": tiles,
                        "encoder_calls": m.encoder_calls},
             "tiles_per_s": round(tiles / wall, 1),
+            "runs_seconds": [round(r[0], 3) for r in runs],
             "encoder_seconds": round(m.encoder_seconds, 3),
             "encoder_share": round(m.encoder_seconds / wall, 4),
             "proxy_loss": m.proxy_loss, "normalized_proxy_loss": m.normalized_proxy_loss,

@@ -735,17 +735,136 @@ __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ leaf,
   return key & 0xFFFFu;
 }
 
-// tb_branch / tb_load for the runtime distance d in [D, row_stride(K)).
+// The decisions of every step that reads one stored row, from one
+// evaluation of the row's depth-D tree. Step i's choice is the key minimum
+// at the top; the level-m reduction computes exactly what step i-1-m
+// chooses between (the FMA over its 2^K predecessors, whose costs are the
+// level below), so if each level reduces keys (cost_bits << 16) | digit
+// instead of bare costs, the choice of step i-1-m for the prefix chosen
+// above is the digit of the level-m key held by that prefix's lane and
+// register (lowest digit on equal costs, as the forward pass). Returns the
+// branches packed: bits [K j, K j + K) hold the branch of step i - j,
+// j = 0..D (K * row_stride(K) <= 10 bits).
 template <int K, int CB, int D>
-__device__ __forceinline__ uint32_t tb_dispatch(int d, const uint16_t* leaf, uint32_t edge,
-                                                const uint16_t* __restrict__ wbits, int ri, int L,
-                                                int lane, int pre) {
-  if constexpr (D + 1 < exl3::row_stride(K)) {
-    if (d != D) return tb_dispatch<K, CB, D + 1>(d, leaf, edge, wbits, ri, L, lane, pre);
+__device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ leaf, uint32_t edge,
+                                            const uint16_t* __restrict__ wbits, int ri, int L,
+                                            int lane) {
+  constexpr int NB = 1 << K, KR = 16 - K, KS = 16 - 2 * K;
+  constexpr int NLOG = K * (D + 1);
+  constexpr int RLOG = NLOG > 6 ? NLOG - 6 : 0;
+  constexpr int R = 1 << RLOG;
+  constexpr uint32_t NMASK = (1u << NLOG) - 1u;
+  constexpr int CH = R < NB ? R : NB;
+  const uint32_t h0 = edge >> K;
+
+  uint32_t nid[R];
+  uint32_t xs[R][D + 1];
+  uint32_t v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t n = (((uint32_t)lane << RLOG) | (uint32_t)r) & NMASK;
+    nid[r] = n;
+    uint32_t x = ((n >> (K * D)) << KS) | h0;
+    xs[r][0] = x;
+#pragma unroll
+    for (int m = 1; m <= D; ++m) {
+      x = (((n >> (K * (D - m))) & (NB - 1)) << KS) | (x >> K);
+      xs[r][m] = x;
+    }
   }
-  return tb_branch<K, CB, D, false>(leaf, edge, wbits, ri, L, lane, pre);
+#pragma unroll
+  for (int c = 0; c < R / CH; ++c) {
+    const typename U16Vec<CH>::type q =
+        *reinterpret_cast<const typename U16Vec<CH>::type*>(leaf + nid[c * CH]);
+#pragma unroll
+    for (int u = 0; u < CH; ++u) v[c * CH + u] = q[u];
+  }
+
+  uint32_t lvl[D > 0 ? D : 1][R];
+#pragma unroll
+  for (int m = D - 1; m >= 0; --m) {
+    const int lo = K * (D - 1 - m), hi = lo + K;
+    int rm = ri - 1 - m;
+    if (rm < 0) rm += L;
+    const f16 wm = f16_bits(wbits[rm]);
+    const int nr = lo < RLOG ? R : 1;  // registers still distinct
+#pragma unroll
+    for (int r = 0; r < nr; ++r) {
+      const uint32_t k = (nid[r] >> lo) & (NB - 1);
+      const f16 dh = decode_state(CB, (k << KR) | xs[r][m]) - wm;
+      v[r] = ((uint32_t)bits_f16(__builtin_fmaf16(dh, dh, f16_bits(v[r]))) << 16) | k;
+    }
+    if (nr == 1) {
+#pragma unroll
+      for (int r = 1; r < R; ++r) v[r] = v[0];
+    }
+#pragma unroll
+    for (int b = lo; b < (hi < RLOG ? hi : RLOG); ++b)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (!(r & (1 << b))) {
+          const uint32_t t = umin(v[r], v[r | (1 << b)]);
+          v[r] = t;
+          v[r | (1 << b)] = t;
+        }
+    if (hi > RLOG) {
+#pragma unroll
+      for (int b = (lo > RLOG ? lo : RLOG); b < (hi < NLOG ? hi : NLOG); ++b)
+        v[0] = xor_min(v[0], 1 << (b - RLOG));
+#pragma unroll
+      for (int r = 1; r < R; ++r) v[r] = v[0];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      lvl[m][r] = v[r];
+      v[r] >>= 16;
+    }
+  }
+
+  // Step i: key minimum over k_0, bits [K D, NLOG) of n.
+  const f16 w = f16_bits(wbits[ri]);
+  const int nr = (K * D) < RLOG ? R : 1;
+  uint32_t key = 0xFFFFFFFFu;
+#pragma unroll
+  for (int r = 0; r < nr; ++r) {
+    const uint32_t k0 = nid[r] >> (K * D);
+    const f16 dh = decode_state(CB, (k0 << KR) | edge) - w;
+    const f16 err = __builtin_fmaf16(dh, dh, f16_bits(v[r]));
+    key = umin(key, ((uint32_t)bits_f16(err) << 16) | k0);
+  }
+#pragma unroll
+  for (int b = (K * D > RLOG ? K * D : RLOG); b < NLOG; ++b)
+    key = xor_min(key, 1 << (b - RLOG));
+  uint32_t prefix = (uint32_t)__builtin_amdgcn_readfirstlane((int)key) & 0xFFFFu;
+  uint32_t ks = prefix;
+#pragma unroll
+  for (int m = 0; m < D; ++m) {
+    const uint32_t nsel = prefix << (K * (D - m));  // the prefix's first leaf
+    const int reg = (int)(nsel & (uint32_t)(R - 1));
+    uint32_t sel = lvl[m][0];
+#pragma unroll
+    for (int r = 1; r < R; ++r)
+      if (r == reg) sel = lvl[m][r];
+    const uint32_t kk =
+        (uint32_t)__builtin_amdgcn_readlane((int)sel, (int)(nsel >> RLOG)) & 0xFFFFu;
+    ks |= kk << (K * (m + 1));
+    prefix = (prefix << K) | kk;
+  }
+  return ks;
 }
 
+template <int K, int CB, int D>
+__device__ __forceinline__ uint32_t tb_tree_dispatch(int d, const uint16_t* leaf, uint32_t edge,
+                                                     const uint16_t* __restrict__ wbits, int ri,
+                                                     int L, int lane) {
+  static_assert(K * exl3::row_stride(K) <= 32, "a row's branches fit in one word");
+  if constexpr (D + 1 < exl3::row_stride(K)) {
+    if (d != D) return tb_tree_dispatch<K, CB, D + 1>(d, leaf, edge, wbits, ri, L, lane);
+  }
+  return tb_tree<K, CB, D>(leaf, edge, wbits, ri, L, lane);
+}
+
+// tb_load for the runtime distance d in [D, row_stride(K)).
 template <int K, int D>
 __device__ __forceinline__ void tb_load_dispatch(int d, const uint16_t* __restrict__ row,
                                                  uint32_t edge, uint16_t* leaf, int lane) {
@@ -755,10 +874,10 @@ __device__ __forceinline__ void tb_load_dispatch(int d, const uint16_t* __restri
   tb_load<K, D>(row, edge, leaf, lane);
 }
 
-// The tree of step i-1 is the subtree of step i's tree under the branch
-// step i chose, so one load of a stored row's tree (at the first step that
-// needs it) serves every step down to that row: the next step's leaves start
-// at base + k * NB^d in LDS. One dependent HBM load per stride of steps.
+// One stored row serves steps i .. r0 + 1: its tree is loaded once, at the
+// first of them, and evaluated once (tb_tree), which yields all of their
+// branches. One dependent HBM load and one tree evaluation per stride of
+// steps.
 template <int K, int CB>
 __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
   constexpr int KR = 16 - K;
@@ -778,37 +897,46 @@ __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
   __syncthreads();
   const uint16_t* wbits = s_wbits;
   uint32_t edge = (uint32_t)a.start[(int64_t)t * a.start_stride] & ((65536u >> K) - 1u);
-  int loaded = -1;  // stored row whose tree is in s_leaf
-  int base = 0;     // offset of the current step's leaves
+  const int i_stop = a.write ? 0 : (L - a.roll) % L;  // the last step walked
 
-  for (int i = L - 1; i >= 0; --i) {
+  int i = L - 1;
+  while (i >= 1 && i >= i_stop) {
+    // Steps i .. r0 + 1 read stored row r0: one tree load, one evaluation.
+    const int d = (i - 1) % STRIDE;
+    const int r0 = i - 1 - d;
+    const uint16_t* row =
+        reinterpret_cast<const uint16_t*>(blk + (int64_t)(r0 / STRIDE) * row_bytes);
+    __syncthreads();  // the previous tree's last readers are done
+    tb_load_dispatch<K, 0>(d, row, edge, s_leaf, lane);
+    __syncthreads();
     int ri = i + a.roll;
     if (ri >= L) ri -= L;
-    uint32_t k;
-    if (i == 0) {
-      k = tb_branch<K, CB, 0, true>(nullptr, edge, wbits, ri, L, lane, pre);
-    } else {
-      const int d = (i - 1) % STRIDE;
-      const int r0 = i - 1 - d;
-      if (r0 != loaded) {
-        const uint16_t* row = reinterpret_cast<const uint16_t*>(
-            blk + (int64_t)(r0 / STRIDE) * row_bytes);
-        __syncthreads();  // the previous tree's last readers are done
-        tb_load_dispatch<K, 0>(d, row, edge, s_leaf, lane);
-        __syncthreads();
-        loaded = r0;
-        base = 0;
+    const uint32_t ks = tb_tree_dispatch<K, CB, 0>(d, s_leaf, edge, wbits, ri, L, lane);
+#pragma unroll
+    for (int j = 0; j < STRIDE; ++j) {
+      if (j <= d && i >= i_stop) {
+        int rj = i + a.roll;
+        if (rj >= L) rj -= L;
+        const uint32_t sigma = (((ks >> (K * j)) & ((1u << K) - 1u)) << KR) | edge;
+        if (a.write && lane == 0) {
+          a.out_idx[(int64_t)t * L + rj] = (int16_t)(uint16_t)sigma;
+          a.out_w[(int64_t)t * L + rj] = (float)decode_state(CB, sigma);
+        }
+        edge = sigma >> K;
+        --i;
       }
-      k = tb_dispatch<K, CB, 0>(d, s_leaf + base, edge, wbits, ri, L, lane, pre);
-      base += (int)k << (K * d);
     }
+  }
+  if (i == 0 && i_stop == 0) {  // step 0: predecessors from the start constraint
+    int ri = a.roll;
+    if (ri >= L) ri -= L;
+    const uint32_t k = tb_branch<K, CB, 0, true>(nullptr, edge, wbits, ri, L, lane, pre);
     const uint32_t sigma = (k << KR) | edge;
     if (a.write && lane == 0) {
       a.out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
       a.out_w[(int64_t)t * L + ri] = (float)decode_state(CB, sigma);
     }
     edge = sigma >> K;
-    if (!a.write && ri == 0) break;
   }
   if (!a.write && lane == 0) a.end_out[(int64_t)t * a.end_stride] = (int32_t)edge;
 }
@@ -901,31 +1029,32 @@ __global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kern
   const uint16_t* wbits = s_wbits;
   uint32_t edge = (uint32_t)a.start[(int64_t)t * a.start_stride] & ((65536u >> K) - 1u);
   int i = L - 1;
-  int base = 0;
   for (int q = 0; q < NR; ++q) {
     if (wave == 0) {
       const uint16_t* row = reinterpret_cast<const uint16_t*>(s_ring[q & 1]);
       const int r = top - q * STRIDE;
-      bool fresh = true;
-      while (i >= last_i && (i - 1) - (i - 1) % STRIDE == r) {
+      if (i >= last_i && (i - 1) - (i - 1) % STRIDE == r) {
+        // Steps i .. r + 1 read this row: one tree, one evaluation.
+        const int d = (i - 1) % STRIDE;
+        tb_load_dispatch<K, 0>(d, row, edge, s_leaf, lane);
+        __builtin_amdgcn_wave_barrier();
         int ri = i + roll;
         if (ri >= L) ri -= L;
-        const int d = (i - 1) % STRIDE;
-        if (fresh) {
-          tb_load_dispatch<K, 0>(d, row, edge, s_leaf, lane);
-          __builtin_amdgcn_wave_barrier();
-          base = 0;
-          fresh = false;
+        const uint32_t ks = tb_tree_dispatch<K, CB, 0>(d, s_leaf, edge, wbits, ri, L, lane);
+#pragma unroll
+        for (int j = 0; j < STRIDE; ++j) {
+          if (j <= d && i >= last_i) {
+            int rj = i + roll;
+            if (rj >= L) rj -= L;
+            const uint32_t sigma = (((ks >> (K * j)) & ((1u << K) - 1u)) << KR) | edge;
+            if (a.write && lane == 0) {
+              s_oidx[rj] = (uint16_t)sigma;
+              s_ow[rj] = (float)decode_state(CB, sigma);
+            }
+            edge = sigma >> K;
+            --i;
+          }
         }
-        const uint32_t k = tb_dispatch<K, CB, 0>(d, s_leaf + base, edge, wbits, ri, L, lane, pre);
-        base += (int)k << (K * d);
-        const uint32_t sigma = (k << KR) | edge;
-        if (a.write && lane == 0) {
-          s_oidx[ri] = (uint16_t)sigma;
-          s_ow[ri] = (float)decode_state(CB, sigma);
-        }
-        edge = sigma >> K;
-        --i;
       }
       __builtin_amdgcn_wave_barrier();  // this tree's readers before the next load
     } else {
