@@ -622,30 +622,6 @@ __device__ __forceinline__ uint32_t row_pos(uint32_t x) {
   return ((x & ((1u << KS) - 1u)) << K) | (x >> KS);
 }
 
-// Leaves of a depth-D tree into LDS: leaf n = (k_0 .. k_D) is C_{r0} at
-// x_D(n), read from the stored row as aligned vectors of sibling costs.
-template <int K, int D>
-__device__ __forceinline__ void tb_load(const uint16_t* __restrict__ row, uint32_t edge,
-                                        uint16_t* leaf, int lane) {
-  constexpr int NB = 1 << K, KS = 16 - 2 * K;
-  constexpr int NLOG = K * (D + 1);
-  constexpr int RLOG = NLOG > 6 ? NLOG - 6 : 0;
-  constexpr int R = 1 << RLOG;
-  constexpr int CH = R < NB ? R : NB;
-  constexpr int NLEAF = 1 << NLOG;
-  const uint32_t h0 = edge >> K;
-  if (((uint32_t)lane << RLOG) >= (uint32_t)NLEAF) return;
-#pragma unroll
-  for (int c = 0; c < R / CH; ++c) {
-    const uint32_t n = ((uint32_t)lane << RLOG) | (uint32_t)(c * CH);
-    uint32_t x = ((n >> (K * D)) << KS) | h0;
-#pragma unroll
-    for (int m = 1; m <= D; ++m) x = (((n >> (K * (D - m))) & (NB - 1)) << KS) | (x >> K);
-    typedef typename U16Vec<CH>::type vec;
-    *reinterpret_cast<vec*>(leaf + n) = *reinterpret_cast<const vec*>(row + row_pos<K>(x));
-  }
-}
-
 template <int K, int CB, int D, bool INIT>
 __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ leaf, uint32_t edge,
                                               const uint16_t* __restrict__ wbits, int ri, int L,
@@ -745,8 +721,12 @@ __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ leaf,
 // register (lowest digit on equal costs, as the forward pass). Returns the
 // branches packed: bits [K j, K j + K) hold the branch of step i - j,
 // j = 0..D (K * row_stride(K) <= 10 bits).
+//
+// The leaves are read straight from the stored row (HBM, or an LDS copy of
+// it): leaf n sits at row_pos(x_D(n)), and a lane's CH leaves that differ
+// only in the last digit are one aligned vector of siblings.
 template <int K, int CB, int D>
-__device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ leaf, uint32_t edge,
+__device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, uint32_t edge,
                                             const uint16_t* __restrict__ wbits, int ri, int L,
                                             int lane) {
   constexpr int NB = 1 << K, KR = 16 - K, KS = 16 - 2 * K;
@@ -774,8 +754,8 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ leaf, u
   }
 #pragma unroll
   for (int c = 0; c < R / CH; ++c) {
-    const typename U16Vec<CH>::type q =
-        *reinterpret_cast<const typename U16Vec<CH>::type*>(leaf + nid[c * CH]);
+    const typename U16Vec<CH>::type q = *reinterpret_cast<const typename U16Vec<CH>::type*>(
+        row + row_pos<K>(xs[c * CH][D]));
 #pragma unroll
     for (int u = 0; u < CH; ++u) v[c * CH + u] = q[u];
   }
@@ -854,24 +834,14 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ leaf, u
 }
 
 template <int K, int CB, int D>
-__device__ __forceinline__ uint32_t tb_tree_dispatch(int d, const uint16_t* leaf, uint32_t edge,
+__device__ __forceinline__ uint32_t tb_tree_dispatch(int d, const uint16_t* row, uint32_t edge,
                                                      const uint16_t* __restrict__ wbits, int ri,
                                                      int L, int lane) {
   static_assert(K * exl3::row_stride(K) <= 32, "a row's branches fit in one word");
   if constexpr (D + 1 < exl3::row_stride(K)) {
-    if (d != D) return tb_tree_dispatch<K, CB, D + 1>(d, leaf, edge, wbits, ri, L, lane);
+    if (d != D) return tb_tree_dispatch<K, CB, D + 1>(d, row, edge, wbits, ri, L, lane);
   }
-  return tb_tree<K, CB, D>(leaf, edge, wbits, ri, L, lane);
-}
-
-// tb_load for the runtime distance d in [D, row_stride(K)).
-template <int K, int D>
-__device__ __forceinline__ void tb_load_dispatch(int d, const uint16_t* __restrict__ row,
-                                                 uint32_t edge, uint16_t* leaf, int lane) {
-  if constexpr (D + 1 < exl3::row_stride(K)) {
-    if (d != D) return tb_load_dispatch<K, D + 1>(d, row, edge, leaf, lane);
-  }
-  tb_load<K, D>(row, edge, leaf, lane);
+  return tb_tree<K, CB, D>(row, edge, wbits, ri, L, lane);
 }
 
 // One stored row serves steps i .. r0 + 1: its tree is loaded once, at the
@@ -882,8 +852,6 @@ template <int K, int CB>
 __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
   constexpr int KR = 16 - K;
   constexpr int STRIDE = exl3::row_stride(K);
-  constexpr int MAXLEAF = 1 << (K * STRIDE);
-  __shared__ __attribute__((aligned(16))) uint16_t s_leaf[MAXLEAF];
   __shared__ uint16_t s_wbits[256];  // the tile's fp16 inputs, ring order
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
@@ -906,12 +874,9 @@ __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
     const int r0 = i - 1 - d;
     const uint16_t* row =
         reinterpret_cast<const uint16_t*>(blk + (int64_t)(r0 / STRIDE) * row_bytes);
-    __syncthreads();  // the previous tree's last readers are done
-    tb_load_dispatch<K, 0>(d, row, edge, s_leaf, lane);
-    __syncthreads();
     int ri = i + a.roll;
     if (ri >= L) ri -= L;
-    const uint32_t ks = tb_tree_dispatch<K, CB, 0>(d, s_leaf, edge, wbits, ri, L, lane);
+    const uint32_t ks = tb_tree_dispatch<K, CB, 0>(d, row, edge, wbits, ri, L, lane);
 #pragma unroll
     for (int j = 0; j < STRIDE; ++j) {
       if (j <= d && i >= i_stop) {
@@ -972,14 +937,12 @@ template <int K, int CB>
 __global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kernel(TbArgs a) {
   constexpr int KR = 16 - K;
   constexpr int STRIDE = exl3::row_stride(K);
-  constexpr int MAXLEAF = 1 << (K * STRIDE);
   constexpr int RV = 2 * (65536 >> K) / 16;  // 16-byte vectors per row
   constexpr int W = StreamShape<K>::W, NG = StreamShape<K>::NG;
   constexpr int NLT = 64 * W;                // threads per loader group
   constexpr int V = RV / NLT;
   static_assert(RV % NLT == 0 && V >= 1, "rows split evenly over a loader group");
   __shared__ u32x4 s_ring[2][RV];
-  __shared__ __attribute__((aligned(16))) uint16_t s_leaf[MAXLEAF];
   __shared__ uint16_t s_wbits[256];
   __shared__ uint16_t s_oidx[256];
   __shared__ float s_ow[256];
@@ -1036,11 +999,9 @@ __global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kern
       if (i >= last_i && (i - 1) - (i - 1) % STRIDE == r) {
         // Steps i .. r + 1 read this row: one tree, one evaluation.
         const int d = (i - 1) % STRIDE;
-        tb_load_dispatch<K, 0>(d, row, edge, s_leaf, lane);
-        __builtin_amdgcn_wave_barrier();
         int ri = i + roll;
         if (ri >= L) ri -= L;
-        const uint32_t ks = tb_tree_dispatch<K, CB, 0>(d, s_leaf, edge, wbits, ri, L, lane);
+        const uint32_t ks = tb_tree_dispatch<K, CB, 0>(d, row, edge, wbits, ri, L, lane);
 #pragma unroll
         for (int j = 0; j < STRIDE; ++j) {
           if (j <= d && i >= last_i) {
@@ -1056,7 +1017,6 @@ __global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kern
           }
         }
       }
-      __builtin_amdgcn_wave_barrier();  // this tree's readers before the next load
     } else {
       const int j = q + 1;  // the row to place in the ring this iteration
       if (j < NR && j % NG == g) {
