@@ -246,6 +246,46 @@ __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const ui
   }
 }
 
+// store_cost_row split around a step's arithmetic (fast kernels): gather
+// the thread's chunks of the row from LDS into registers when the step
+// starts, write them to HBM when its arithmetic is done, so the gather's LDS
+// latency overlaps the step instead of delaying it. CPT chunks per thread
+// (E / 8 chunks over NT threads, first threads first).
+template <int K, int NT, int KS, int PAD>
+struct RowGather {
+  static constexpr int CHUNKS = (65536 >> K) / 8;
+  static constexpr int CPT = (CHUNKS + NT - 1) / NT;
+  uint32_t v[CPT][4];
+
+  __device__ __forceinline__ void gather(const uint16_t* src) {
+    constexpr int ks = 16 - 2 * K;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int c = threadIdx.x + j * NT;
+      if (CHUNKS % NT == 0 || c < CHUNKS) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int t0 = 8 * c + 2 * m, t1 = t0 + 1;
+          const uint32_t lo = src[lds_pos<KS, PAD>(((t0 & ((1 << K) - 1)) << ks) | (t0 >> K))];
+          const uint32_t hi = src[lds_pos<KS, PAD>(((t1 & ((1 << K) - 1)) << ks) | (t1 >> K))];
+          v[j][m] = lo | (hi << 16);
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void commit(const FwdArgs& a, int step) const {
+    const BpLayout lay = exl3::make_layout(K);
+    uint4* dst = reinterpret_cast<uint4*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
+                                          (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int c = threadIdx.x + j * NT;
+      if (CHUNKS % NT == 0 || c < CHUNKS) dst[c] = make_uint4(v[j][0], v[j][1], v[j][2], v[j][3]);
+    }
+  }
+};
+
 // Whether forward step i stores the cost row of step i - 1.
 __device__ __forceinline__ bool stores_row(const FwdArgs& a, int K, int i) {
   return i >= 1 && i - 1 >= a.store_from && exl3::cost_row_stored(exl3::make_layout(K), i - 1);
@@ -364,7 +404,9 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
     if (ri >= L) ri -= L;
     const uint16_t* cin = s_cost[i & 1];
     uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[(i & 1) ^ 1]);
-    if (stores_row(a, K, i)) store_cost_row<C::NT, KS, PAD>(a, K, cin, i - 1);
+    const bool store = stores_row(a, K, i);
+    RowGather<K, C::NT, KS, PAD> row;
+    if (store) row.gather(cin);
     const f16 w = s_w[ri];
     f16x2 w2;
     w2.x = w;
@@ -417,6 +459,7 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
         const int e = (grp(g) << K) | (jj * J + 2 * jp);
         if (P == 1 || p == 0) cout[lds_pos<KS, PAD>(e) >> 1] = __builtin_bit_cast(uint32_t, v);
       }
+    if (store) row.commit(a, i - 1);
     __syncthreads();
   }
   forward_epilogue<C::NT, KS, PAD>(a, C::E, s_cost[L & 1], s_red);
