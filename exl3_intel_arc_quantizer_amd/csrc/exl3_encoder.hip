@@ -405,8 +405,6 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
     const uint16_t* cin = s_cost[i & 1];
     uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[(i & 1) ^ 1]);
     const bool store = stores_row(a, K, i);
-    RowGather<K, C::NT, KS, PAD> row;
-    if (store) row.gather(cin);
     const f16 w = s_w[ri];
     f16x2 w2;
     w2.x = w;
@@ -459,7 +457,12 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
         const int e = (grp(g) << K) | (jj * J + 2 * jp);
         if (P == 1 || p == 0) cout[lds_pos<KS, PAD>(e) >> 1] = __builtin_bit_cast(uint32_t, v);
       }
-    if (store) row.commit(a, i - 1);
+    if (store) {
+      // cin stays intact until the barrier: gather after the arithmetic.
+      RowGather<K, C::NT, KS, PAD> row;
+      row.gather(cin);
+      row.commit(a, i - 1);
+    }
     __syncthreads();
   }
   forward_epilogue<C::NT, KS, PAD>(a, C::E, s_cost[L & 1], s_red);
