@@ -246,42 +246,41 @@ __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const ui
   }
 }
 
-// store_cost_row split around a step's arithmetic (fast kernels): gather
-// the thread's chunks of the row from LDS into registers when the step
-// starts, write them to HBM when its arithmetic is done, so the gather's LDS
-// latency overlaps the step instead of delaying it. CPT chunks per thread
-// (E / 8 chunks over NT threads, first threads first).
+// store_cost_row for the fast kernels, run after a step's arithmetic (the
+// stored row, the step's input, stays intact until the barrier). The row is
+// cut into pieces of W consecutive positions, the first threads taking one
+// or more pieces each; a wave's global store stays contiguous. W = 8
+// (16-byte stores) up to K = 5; at K = 6, 7, where 16-byte pieces would
+// leave the row to one or two waves, W = 2 spreads it over 4-8 waves
+// (measured: K = 6 92 -> 94 % of the VALU peak; 4-byte pieces at K = 4, 5
+// measured slower).
 template <int K, int NT, int KS, int PAD>
 struct RowGather {
-  static constexpr int CHUNKS = (65536 >> K) / 8;
-  static constexpr int CPT = (CHUNKS + NT - 1) / NT;
-  uint32_t v[CPT][4];
+  static constexpr int E = 65536 >> K;
+  static constexpr int W = K >= 6 ? 2 : 8;                                   // positions per piece
+  static constexpr int PIECES = E / W;
+  static constexpr int PPT = (PIECES + NT - 1) / NT;                       // pieces per thread
+  typedef uint32_t vec __attribute__((ext_vector_type(W / 2)));
 
-  __device__ __forceinline__ void gather(const uint16_t* src) {
+  __device__ __forceinline__ static void store(const FwdArgs& a, const uint16_t* src, int step) {
     constexpr int ks = 16 - 2 * K;
+    const BpLayout lay = exl3::make_layout(K);
+    vec* dst = reinterpret_cast<vec*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
+                                      (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
+    for (int j = 0; j < PPT; ++j) {
       const int c = threadIdx.x + j * NT;
-      if (CHUNKS % NT == 0 || c < CHUNKS) {
+      if (PIECES % NT == 0 || c < PIECES) {
+        vec v;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const int t0 = 8 * c + 2 * m, t1 = t0 + 1;
+        for (int m = 0; m < W / 2; ++m) {
+          const int t0 = W * c + 2 * m, t1 = t0 + 1;
           const uint32_t lo = src[lds_pos<KS, PAD>(((t0 & ((1 << K) - 1)) << ks) | (t0 >> K))];
           const uint32_t hi = src[lds_pos<KS, PAD>(((t1 & ((1 << K) - 1)) << ks) | (t1 >> K))];
-          v[j][m] = lo | (hi << 16);
+          v[m] = lo | (hi << 16);
         }
+        dst[c] = v;
       }
-    }
-  }
-
-  __device__ __forceinline__ void commit(const FwdArgs& a, int step) const {
-    const BpLayout lay = exl3::make_layout(K);
-    uint4* dst = reinterpret_cast<uint4*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
-                                          (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int c = threadIdx.x + j * NT;
-      if (CHUNKS % NT == 0 || c < CHUNKS) dst[c] = make_uint4(v[j][0], v[j][1], v[j][2], v[j][3]);
     }
   }
 };
@@ -457,12 +456,7 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
         const int e = (grp(g) << K) | (jj * J + 2 * jp);
         if (P == 1 || p == 0) cout[lds_pos<KS, PAD>(e) >> 1] = __builtin_bit_cast(uint32_t, v);
       }
-    if (store) {
-      // cin stays intact until the barrier: gather after the arithmetic.
-      RowGather<K, C::NT, KS, PAD> row;
-      row.gather(cin);
-      row.commit(a, i - 1);
-    }
+    if (store) RowGather<K, C::NT, KS, PAD>::store(a, cin, i - 1);
     __syncthreads();
   }
   forward_epilogue<C::NT, KS, PAD>(a, C::E, s_cost[L & 1], s_red);
