@@ -12,17 +12,23 @@
 //                      candidate pair plus v_pk_minimum3_f16 folding two pairs
 //                      per instruction: the minimum cost per edge only. Every
 //                      row_stride(K)-th cost row goes to HBM (group-major,
-//                      coalesced 16-byte stores); the traceback recomputes the
-//                      argmin of the one edge on the path.
+//                      coalesced stores after the step's arithmetic); the
+//                      traceback recomputes the argmin of the one edge on
+//                      the path.
 //   acs_forward_generic reference-structured kernel (one edge per thread
 //                      iteration, codebook decoded per candidate, strict fp16
 //                      '<' scan): K = 8 and the force_global_costs variant;
 //                      writes the same scratch layout as the fast kernels.
 //   traceback_rows_kernel one 64-lane workgroup per tile walks the ring
-//                      backwards, rebuilding the costs of unstored steps from
-//                      the last stored row; traceback_bp_kernel (K = 8) reads
-//                      one backpointer byte per step.
-//   finalize_kernel    packing, path cost, distortion, un-permutation.
+//                      backwards; one evaluation of each stored row's tree
+//                      (rebuilding the costs of the unstored steps) yields
+//                      the branches of every step that reads that row.
+//   traceback_stream_kernel the same walk for small batches, with every
+//                      stored row prefetched whole into an LDS ring by
+//                      loader waves; traceback_bp_kernel (K = 8) reads one
+//                      backpointer byte per step.
+//   finalize_kernel    packing, path cost, distortion, un-permutation;
+//   unpack_kernel      the inverse of the packing (stored-tensor read-back).
 //
 // Numerics (bit-exact vs the reference on finite / infinite inputs):
 //   dh = fp16(val - w) (v_pk_add_f16), err = fma_f16(dh, dh, cost_prev)
@@ -36,7 +42,7 @@
 //   (cost_bits << 16 | k) picks the lowest k among equal minima — the
 //   reference's "k = 0 initialises, later k replaces only if strictly
 //   smaller" rule (reference_encoder.py:169-176,193-199). NaN inputs are
-//   rejected by the host wrapper (see the package's encoder module).
+//   counted by prepare_kernel and rejected by the host wrapper.
 #include <hip/hip_runtime.h>
 
 #include <stdarg.h>
@@ -75,6 +81,15 @@ static int set_error(const char* fmt, ...) {
 static int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+  return 0;
+}
+
+// Blocks of `block` threads covering `total` elements of a 1-D launch, or
+// an error when that exceeds the grid limit.
+static int grid_1d(int64_t total, int block, unsigned* blocks, const char* what) {
+  const int64_t b = (total + block - 1) / block;
+  if (total <= 0 || b > (int64_t)INT32_MAX) return set_error("%s: batch too large", what);
+  *blocks = (unsigned)b;
   return 0;
 }
 
@@ -1534,10 +1549,12 @@ int exl3_prepare_tiles(const float* raw, float* out, int64_t n, int L, int permu
                        int32_t* nan_count, void* stream) {
   if (n <= 0 || L <= 0) return set_error("bad tile batch shape");
   if (permute && L != 256) return set_error("pre_permute=True is only defined for L=256");
-  const int64_t total = n * L;
+  if (!raw || !out) return set_error("NULL buffer");
   const int block = 256;
-  hipLaunchKernelGGL(prepare_kernel, dim3((unsigned)((total + block - 1) / block)), dim3(block), 0,
-                     as_stream(stream), raw, out, n, L, permute, nan_count);
+  unsigned blocks;
+  if (grid_1d(n * L, block, &blocks, "prepare_tiles")) return 1;
+  hipLaunchKernelGGL(prepare_kernel, dim3(blocks), dim3(block), 0, as_stream(stream), raw, out, n,
+                     L, permute, nan_count);
   return check_launch("prepare_tiles");
 }
 
@@ -1556,29 +1573,36 @@ int exl3_finalize_tiles(const float* x, const float* raw, const float* out_w,
 
 int exl3_pack_trellis(const int16_t* states, uint16_t* packed, int64_t n, int K, void* stream) {
   if (n <= 0 || K < 1 || K > 8) return set_error("bad pack arguments");
-  const int64_t total = n * 16;
+  if (!states || !packed) return set_error("NULL buffer");
   const int block = 256;
-  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((total + block - 1) / block)), dim3(block), 0,
-                     as_stream(stream), states, packed, n, K);
+  unsigned blocks;
+  if (grid_1d(n * 16, block, &blocks, "pack_trellis")) return 1;
+  hipLaunchKernelGGL(pack_kernel, dim3(blocks), dim3(block), 0, as_stream(stream), states, packed,
+                     n, K);
   return check_launch("pack_trellis");
 }
 
 int exl3_unpack_trellis(const uint16_t* packed, int16_t* states, int64_t n, int K, void* stream) {
   if (n <= 0 || K < 1 || K > 8) return set_error("bad unpack arguments");
   if (!packed || !states) return set_error("NULL buffer");
-  const int64_t total = n * 256;
   const int block = 256;
-  hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)((total + block - 1) / block)), dim3(block), 0,
-                     as_stream(stream), packed, states, n, K);
+  unsigned blocks;
+  if (grid_1d(n * 256, block, &blocks, "unpack_trellis")) return 1;
+  hipLaunchKernelGGL(unpack_kernel, dim3(blocks), dim3(block), 0, as_stream(stream), packed,
+                     states, n, K);
   return check_launch("unpack_trellis");
 }
 
 int exl3_probe_hfma(const uint16_t* a, const uint16_t* c, uint16_t* out, int64_t n, int mode,
                     void* stream) {
   if (n <= 0) return set_error("n must be positive");
+  if (mode != 0 && mode != 1) return set_error("mode must be 0 or 1, got %d", mode);
+  if (!a || !c || !out) return set_error("NULL buffer");
   const int block = 256;
-  hipLaunchKernelGGL(probe_hfma_kernel, dim3((unsigned)((n + block - 1) / block)), dim3(block), 0,
-                     as_stream(stream), a, c, out, n, mode);
+  unsigned blocks;
+  if (grid_1d(n, block, &blocks, "probe_hfma")) return 1;
+  hipLaunchKernelGGL(probe_hfma_kernel, dim3(blocks), dim3(block), 0, as_stream(stream), a, c, out,
+                     n, mode);
   return check_launch("probe_hfma");
 }
 

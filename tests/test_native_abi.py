@@ -103,6 +103,21 @@ def test_forward_and_backward_reject_bad_arguments():
     assert lib.exl3_pack_trellis(None, None, 0, 2, None) != 0
     assert lib.exl3_prepare_tiles(None, None, 1, 160, 1, None, None) != 0
     assert "pre_permute" in lib.exl3_last_error().decode()
+    # Valid shapes with NULL device buffers are refused, never launched.
+    assert lib.exl3_decode_codebook(2, None, None) != 0
+    assert lib.exl3_prepare_tiles(None, None, 4, 256, 0, None, None) != 0
+    assert b"NULL" in lib.exl3_last_error()
+    assert lib.exl3_pack_trellis(None, None, 4, 2, None) != 0
+    assert lib.exl3_unpack_trellis(None, None, 4, 2, None) != 0
+    assert lib.exl3_probe_hfma(None, None, None, 4, 0, None) != 0
+    assert lib.exl3_probe_hfma(None, None, None, 4, 7, None) != 0
+    assert b"mode" in lib.exl3_last_error()
+    assert lib.exl3_finalize_tiles(None, None, None, None, None, None, None, None, 4, 2, 256, 0,
+                                   None) != 0
+    assert lib.exl3_forward_pass(None, None, None, None, 4, 2, 2, 256, 0, 0, 0, None) != 0
+    assert lib.exl3_backward_pass(None, None, None, None, None, 4, 2, 2, 256, 0, 0, 1, None) != 0
+    assert lib.exl3_quantize_tiles(None, None, None, None, None, 4, 4, 2, 2, 256, 0, 0, None) != 0
+    assert b"NULL" in lib.exl3_last_error()
 
 
 def test_traceback_policy_switch():
