@@ -199,16 +199,24 @@ struct FwdArgs {
 };
 
 // Load the tile's fp16 inputs into LDS, record pre_state (and, for cost rows,
-// the inputs) in the tile header, and set the initial cost vector.
+// the inputs) in the tile header, and set the initial cost vector. s_w is in
+// ring order (s_w[ri]), or with step_order in step order (s_w[i] = input
+// (i + roll) mod L).
 template <int NT, int KS = 0, int PAD = 0>
 __device__ __forceinline__ void forward_prologue(const FwdArgs& a, int E, bool stash_inputs,
-                                                 f16* s_w, uint16_t* cost0, int& pre_out) {
+                                                 f16* s_w, uint16_t* cost0, int& pre_out,
+                                                 bool step_order = false) {
   const int tile = blockIdx.x;
   const float* in = a.in + (int64_t)tile * a.L;
   uint8_t* hdr = a.scratch + (int64_t)tile * a.tile_stride + a.hdr_offset;
   for (int r = threadIdx.x; r < a.L; r += NT) {
     const f16 w = (f16)in[r];
-    s_w[r] = w;
+    int slot = r;
+    if (step_order) {
+      slot = r - a.roll;
+      if (slot < 0) slot += a.L;
+    }
+    s_w[slot] = w;
     if (stash_inputs) reinterpret_cast<uint16_t*>(hdr + exl3::HDR_W_BYTES)[r] = bits_f16(w);
   }
   const int pre = a.pre_states ? a.pre_states[(int64_t)tile * a.pre_stride] : -1;
@@ -311,6 +319,24 @@ __device__ __forceinline__ bool stores_row(const FwdArgs& a, int K, int i) {
   return i >= 1 && i - 1 >= a.store_from && exl3::cost_row_stored(exl3::make_layout(K), i - 1);
 }
 
+// stores_row for a step of known parity (i = 2 p + B): rows are stored at
+// steps i - 1 that are multiples of an even stride, so an even step never
+// stores one unless the stride is 1.
+template <int K, int B>
+__device__ __forceinline__ bool stores_row_at(const FwdArgs& a, int i) {
+  constexpr int STRIDE = exl3::row_stride(K);
+  if constexpr (STRIDE > 1 && B == 0) {
+    return false;
+  } else {
+    return i - 1 >= a.store_from && (STRIDE <= 2 || (i - 1) % STRIDE == 0);
+  }
+}
+
+template <int V>
+struct Phase {
+  static constexpr int value = V;
+};
+
 // ------------------------------------------------------------ fast kernels
 
 // Thread decomposition per K (exl3_layout.h keeps the same table): G groups x
@@ -382,7 +408,7 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
   static_assert(C::Q % 2 == 0, "branches are folded two at a time");
   static_assert(PAD == 0 || G == 1, "padding keeps group pairs of G > 1 together");
   __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][EP];
-  __shared__ f16 s_w[256];
+  __shared__ __attribute__((aligned(4))) f16 s_w[256];
   __shared__ uint32_t s_red[16];
 
   const int L = a.L;
@@ -416,16 +442,16 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
         cbv[g][jp][q] = v;
       }
   int pre;
-  forward_prologue<C::NT, KS, PAD>(a, C::E, true, s_w, s_cost[0], pre);
+  forward_prologue<C::NT, KS, PAD>(a, C::E, true, s_w, s_cost[0], pre, true);
   __syncthreads();
 
-  for (int i = 0; i < L; ++i) {
-    int ri = i + a.roll;
-    if (ri >= L) ri -= L;
-    const uint16_t* cin = s_cost[i & 1];
-    uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[(i & 1) ^ 1]);
-    const bool store = stores_row(a, K, i);
-    const f16 w = s_w[ri];
+  // One step; B = i & 1 is the ping-pong phase, fixed at compile time so
+  // every LDS address is a per-thread base plus an immediate offset.
+  auto step = [&](auto phase, int i, f16 w) {
+    constexpr int B = decltype(phase)::value;
+    const uint16_t* cin = s_cost[B];
+    uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[B ^ 1]);
+    const bool store = i >= 1 && stores_row_at<K, B>(a, i);
     f16x2 w2;
     w2.x = w;
     w2.y = w;
@@ -479,8 +505,14 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
       }
     if (store) RowGather<K, C::NT, KS, PAD>::store(a, cin, i - 1);
     __syncthreads();
+  };
+  // L is even: steps go in pairs, whose inputs are one aligned 32-bit read.
+  for (int i = 0; i < L; i += 2) {
+    const f16x2 wp = *reinterpret_cast<const f16x2*>(&s_w[i]);
+    step(Phase<0>(), i, wp.x);
+    step(Phase<1>(), i + 1, wp.y);
   }
-  forward_epilogue<C::NT, KS, PAD>(a, C::E, s_cost[L & 1], s_red);
+  forward_epilogue<C::NT, KS, PAD>(a, C::E, s_cost[0], s_red);
 }
 
 // --------------------------------------------------------- generic kernel
