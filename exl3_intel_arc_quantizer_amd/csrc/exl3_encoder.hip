@@ -295,12 +295,37 @@ struct RowGather {
       const int c = threadIdx.x + j * NT;
       if (PIECES % NT == 0 || c < PIECES) {
         vec v;
+        if constexpr (K == 2 && PAD == 0) {
+          // Positions 8c + u and 8c + u + 4 are LDS neighbours (2c, 2c + 1
+          // of block u): four dword reads, halves interleaved by v_perm.
+          const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
+          uint32_t r[4];
 #pragma unroll
-        for (int m = 0; m < W / 2; ++m) {
-          const int t0 = W * c + 2 * m, t1 = t0 + 1;
-          const uint32_t lo = src[lds_pos<KS, PAD>(((t0 & ((1 << K) - 1)) << ks) | (t0 >> K))];
-          const uint32_t hi = src[lds_pos<KS, PAD>(((t1 & ((1 << K) - 1)) << ks) | (t1 >> K))];
-          v[m] = lo | (hi << 16);
+          for (int u = 0; u < 4; ++u) r[u] = s32[((u << ks) | (2 * c)) >> 1];
+          v[0] = __builtin_amdgcn_perm(r[1], r[0], 0x05040100u);
+          v[1] = __builtin_amdgcn_perm(r[3], r[2], 0x05040100u);
+          v[2] = __builtin_amdgcn_perm(r[1], r[0], 0x07060302u);
+          v[3] = __builtin_amdgcn_perm(r[3], r[2], 0x07060302u);
+        } else if constexpr (K == 1 && PAD == 0) {
+          // Even positions 8c + 2m from block 0, odd ones from block 1, each
+          // four LDS neighbours (4c .. 4c + 3): two 8-byte reads.
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 e = *reinterpret_cast<const u32x2*>(src + 4 * c);
+          const u32x2 o = *reinterpret_cast<const u32x2*>(src + (1 << ks) + 4 * c);
+          v[0] = __builtin_amdgcn_perm(o.x, e.x, 0x05040100u);
+          v[1] = __builtin_amdgcn_perm(o.x, e.x, 0x07060302u);
+          v[2] = __builtin_amdgcn_perm(o.y, e.y, 0x05040100u);
+          v[3] = __builtin_amdgcn_perm(o.y, e.y, 0x07060302u);
+        } else {
+#pragma unroll
+          for (int m = 0; m < W / 2; ++m) {
+            const int t0 = W * c + 2 * m, t1 = t0 + 1;
+            const uint32_t lo =
+                src[lds_pos<KS, PAD>(((t0 & ((1 << K) - 1)) << ks) | (t0 >> K))];
+            const uint32_t hi =
+                src[lds_pos<KS, PAD>(((t1 & ((1 << K) - 1)) << ks) | (t1 >> K))];
+            v[m] = lo | (hi << 16);
+          }
         }
         // K <= 3 write 8 KiB of rows per step (2.7 TB/s at 4096 tiles):
         // streaming stores there measured 80-83 -> 88 % (K = 2) and
