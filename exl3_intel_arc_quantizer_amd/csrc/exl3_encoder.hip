@@ -242,8 +242,8 @@ __device__ __forceinline__ void forward_epilogue(const FwdArgs& a, int E, const 
 }
 
 // Copy the cost row of step `step` (held in LDS in edge order) to its slot
-// in the tile's scratch, group-major (exl3::cost_row_pos): position t holds
-// edge (k << (16-2K)) | h for t = (h << K) | k. 16-byte chunk c covers
+// in the tile's scratch: position t holds edge exl3::cost_row_edge(K, t)
+// (group-major, (h << K) | k for edge (k << (16-2K)) | h). 16-byte chunk c covers
 // positions 8c .. 8c + 7, gathered from LDS; the global stores stay
 // contiguous. The chunks go to the first E / 8 threads: leaving the other
 // waves free measured faster than spreading the gather over every wave.
@@ -252,7 +252,6 @@ __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const ui
                                                int step) {
   const BpLayout lay = exl3::make_layout(K);
   const int E = 65536 >> K;
-  const int ks = 16 - 2 * K;
   const int chunks = E / 8;
   uint4* dst = reinterpret_cast<uint4*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
                                         (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
@@ -261,8 +260,8 @@ __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const ui
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int t0 = 8 * c + 2 * m, t1 = t0 + 1;
-      const uint32_t lo = src[lds_pos<KS, PAD>(((t0 & ((1 << K) - 1)) << ks) | (t0 >> K))];
-      const uint32_t hi = src[lds_pos<KS, PAD>(((t1 & ((1 << K) - 1)) << ks) | (t1 >> K))];
+      const uint32_t lo = src[lds_pos<KS, PAD>(exl3::cost_row_edge(K, t0))];
+      const uint32_t hi = src[lds_pos<KS, PAD>(exl3::cost_row_edge(K, t1))];
       v[m] = lo | (hi << 16);
     }
     dst[c] = make_uint4(v[0], v[1], v[2], v[3]);
@@ -290,23 +289,31 @@ struct RowGather {
     const BpLayout lay = exl3::make_layout(K);
     vec* dst = reinterpret_cast<vec*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
                                       (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
+    if constexpr (K == 2 && PAD == 0 && NT == PIECES / 2) {
+      // Positions t and t + 8192 hold the LDS neighbours x and x + 1
+      // (x even): thread c takes pieces c and c + NT from eight dword reads,
+      // their halves sorted into the two pieces by v_perm.
+      const int c = threadIdx.x;
+      const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
+      uint32_t r[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) r[u] = s32[exl3::cost_row_edge(K, 8 * c + u) >> 1];
+      vec lo, hi;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        lo[m] = __builtin_amdgcn_perm(r[2 * m + 1], r[2 * m], 0x05040100u);
+        hi[m] = __builtin_amdgcn_perm(r[2 * m + 1], r[2 * m], 0x07060302u);
+      }
+      __builtin_nontemporal_store(lo, &dst[c]);
+      __builtin_nontemporal_store(hi, &dst[c + NT]);
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
       const int c = threadIdx.x + j * NT;
       if (PIECES % NT == 0 || c < PIECES) {
         vec v;
-        if constexpr (K == 2 && PAD == 0) {
-          // Positions 8c + u and 8c + u + 4 are LDS neighbours (2c, 2c + 1
-          // of block u): four dword reads, halves interleaved by v_perm.
-          const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
-          uint32_t r[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) r[u] = s32[((u << ks) | (2 * c)) >> 1];
-          v[0] = __builtin_amdgcn_perm(r[1], r[0], 0x05040100u);
-          v[1] = __builtin_amdgcn_perm(r[3], r[2], 0x05040100u);
-          v[2] = __builtin_amdgcn_perm(r[1], r[0], 0x07060302u);
-          v[3] = __builtin_amdgcn_perm(r[3], r[2], 0x07060302u);
-        } else if constexpr (K == 1 && PAD == 0) {
+        if constexpr (K == 1 && PAD == 0) {
           // Even positions 8c + 2m from block 0, odd ones from block 1, each
           // four LDS neighbours (4c .. 4c + 3): two 8-byte reads.
           typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -320,10 +327,8 @@ struct RowGather {
 #pragma unroll
           for (int m = 0; m < W / 2; ++m) {
             const int t0 = W * c + 2 * m, t1 = t0 + 1;
-            const uint32_t lo =
-                src[lds_pos<KS, PAD>(((t0 & ((1 << K) - 1)) << ks) | (t0 >> K))];
-            const uint32_t hi =
-                src[lds_pos<KS, PAD>(((t1 & ((1 << K) - 1)) << ks) | (t1 >> K))];
+            const uint32_t lo = src[lds_pos<KS, PAD>(exl3::cost_row_edge(K, t0))];
+            const uint32_t hi = src[lds_pos<KS, PAD>(exl3::cost_row_edge(K, t1))];
             v[m] = lo | (hi << 16);
           }
         }
@@ -736,8 +741,7 @@ struct U16Vec {
 
 template <int K>
 __device__ __forceinline__ uint32_t row_pos(uint32_t x) {
-  constexpr int KS = 16 - 2 * K;
-  return ((x & ((1u << KS) - 1u)) << K) | (x >> KS);
+  return exl3::cost_row_pos(K, x);
 }
 
 template <int K, int CB, int D, bool INIT>

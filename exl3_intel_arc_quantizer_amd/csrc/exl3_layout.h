@@ -20,7 +20,8 @@
 //   recomputes the 2^K candidates of the one edge on the path from the costs
 //   of step i-1 (the costs the forward step i read). A row is group-major:
 //   predecessor edge x = (k << (16-2K)) | h sits at position (h << K) | k,
-//   so the 2^K costs one traceback step reads are one contiguous chunk.
+//   so the 2^K costs one traceback step reads are one contiguous chunk
+//   (K = 2 also keeps the digit before next to it, see cost_row_pos).
 //   Only every row_stride(K)-th step is stored (8 KiB or less of HBM writes
 //   per step at K <= 5); for a step d rows past the last stored one, the
 //   traceback rebuilds the costs it needs level by level, each a minimum
@@ -104,9 +105,24 @@ EXL3_HD inline BpLayout make_layout(int K) {
 // Cost rows: which steps are stored, where, and where edge x sits in a row.
 EXL3_HD inline bool cost_row_stored(const BpLayout& l, int step) { return step % l.stride == 0; }
 EXL3_HD inline int cost_row_slot(const BpLayout& l, int step) { return step / l.stride; }
+// Group-major: x = (k << (16-2K)) | h at (h << K) | k. K = 2, where a
+// stored row serves four steps and a traceback tree has 256 leaves, also
+// puts the digit before k next to it: x bits 12-13 at positions 0-1, bits
+// 10-11 at 2-3, bits 1-9 at 4-12 and bit 0 at 13. A four-step tree then
+// spans 16 runs of 16 positions instead of 64 runs of 4, and positions t
+// and t + 8192 hold the neighbouring edges x and x + 1.
 EXL3_HD inline uint32_t cost_row_pos(int K, uint32_t x) {
+  if (K == 2)
+    return (x >> 12) | (((x >> 10) & 3u) << 2) | (((x >> 1) & 511u) << 4) | ((x & 1u) << 13);
   const int ks = 16 - 2 * K;
   return ((x & ((1u << ks) - 1u)) << K) | (x >> ks);
+}
+// The edge at position t of a stored row (the inverse of cost_row_pos).
+EXL3_HD inline uint32_t cost_row_edge(int K, uint32_t t) {
+  if (K == 2)
+    return ((t & 3u) << 12) | (((t >> 2) & 3u) << 10) | (((t >> 4) & 511u) << 1) | (t >> 13);
+  const int ks = 16 - 2 * K;
+  return ((t & ((1u << K) - 1u)) << ks) | (t >> K);
 }
 // First row the pass-1 traceback reaches: it covers steps L-1 .. L/2 and
 // needs the stored row at or before L/2 - 1.
