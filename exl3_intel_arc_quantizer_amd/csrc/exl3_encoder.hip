@@ -289,23 +289,32 @@ struct RowGather {
     const BpLayout lay = exl3::make_layout(K);
     vec* dst = reinterpret_cast<vec*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
                                       (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
-    if constexpr (K == 2 && PAD == 0 && NT == PIECES / 2) {
-      // Positions t and t + 8192 hold the LDS neighbours x and x + 1
-      // (x even): thread c takes pieces c and c + NT from eight dword reads,
-      // their halves sorted into the two pieces by v_perm.
+    if constexpr (exl3::cost_row_tree_bits(K) > 0 && PAD == 0 && W == 8) {
+      // Positions t and t + E/2 hold the LDS neighbours x and x + 1 (x
+      // even): thread c < E/16 takes pieces c and c + E/16 from eight dword
+      // reads, their halves sorted into the two pieces by v_perm.
+      constexpr int HALF = PIECES / 2;
+      static_assert(HALF <= NT, "one pair of pieces per thread");
       const int c = threadIdx.x;
-      const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
-      uint32_t r[8];
+      if (HALF == NT || c < HALF) {
+        const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
+        uint32_t r[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) r[u] = s32[exl3::cost_row_edge(K, 8 * c + u) >> 1];
-      vec lo, hi;
+        for (int u = 0; u < 8; ++u) r[u] = s32[exl3::cost_row_edge(K, 8 * c + u) >> 1];
+        vec lo, hi;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        lo[m] = __builtin_amdgcn_perm(r[2 * m + 1], r[2 * m], 0x05040100u);
-        hi[m] = __builtin_amdgcn_perm(r[2 * m + 1], r[2 * m], 0x07060302u);
+        for (int m = 0; m < 4; ++m) {
+          lo[m] = __builtin_amdgcn_perm(r[2 * m + 1], r[2 * m], 0x05040100u);
+          hi[m] = __builtin_amdgcn_perm(r[2 * m + 1], r[2 * m], 0x07060302u);
+        }
+        if constexpr (K <= 3) {
+          __builtin_nontemporal_store(lo, &dst[c]);
+          __builtin_nontemporal_store(hi, &dst[c + HALF]);
+        } else {
+          dst[c] = lo;
+          dst[c + HALF] = hi;
+        }
       }
-      __builtin_nontemporal_store(lo, &dst[c]);
-      __builtin_nontemporal_store(hi, &dst[c + NT]);
       return;
     }
 #pragma unroll

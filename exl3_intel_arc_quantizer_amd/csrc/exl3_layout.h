@@ -21,7 +21,8 @@
 //   of step i-1 (the costs the forward step i read). A row is group-major:
 //   predecessor edge x = (k << (16-2K)) | h sits at position (h << K) | k,
 //   so the 2^K costs one traceback step reads are one contiguous chunk
-//   (K = 2 also keeps the digit before next to it, see cost_row_pos).
+//   (K = 2..5 also keep part of the digit before beside it, see
+//   cost_row_pos).
 //   Only every row_stride(K)-th step is stored (8 KiB or less of HBM writes
 //   per step at K <= 5); for a step d rows past the last stored one, the
 //   traceback rebuilds the costs it needs level by level, each a minimum
@@ -105,24 +106,40 @@ EXL3_HD inline BpLayout make_layout(int K) {
 // Cost rows: which steps are stored, where, and where edge x sits in a row.
 EXL3_HD inline bool cost_row_stored(const BpLayout& l, int step) { return step % l.stride == 0; }
 EXL3_HD inline int cost_row_slot(const BpLayout& l, int step) { return step / l.stride; }
-// Group-major: x = (k << (16-2K)) | h at (h << K) | k. K = 2, where a
-// stored row serves four steps and a traceback tree has 256 leaves, also
-// puts the digit before k next to it: x bits 12-13 at positions 0-1, bits
-// 10-11 at 2-3, bits 1-9 at 4-12 and bit 0 at 13. A four-step tree then
-// spans 16 runs of 16 positions instead of 64 runs of 4, and positions t
-// and t + 8192 hold the neighbouring edges x and x + 1.
+// Group-major: x = (k << (16-2K)) | h at (h << K) | k, so the 2^K costs a
+// traceback step compares are one chunk. At K = 2..5, where a stored row
+// serves several steps and one traceback tree spans 2^(K * (stride + 1))
+// entries, the row also keeps part of the digit before k beside it: the
+// last digit (x >> (16-2K)) at positions [0, K), then the lowest
+// cost_row_tree_bits(K) bits of the digit before it, then the other bits of
+// x from bit 1 up, and x bit 0 on top. A tree then covers 16 (K = 2, 5) or
+// 4 (K = 3, 4) cache lines instead of 64, 8, 16 or 32, and positions t and
+// t + E/2 hold the neighbouring edges x and x + 1 (one dword in LDS). More
+// bits of that digit would put the forward pass's LDS gather into bank
+// conflicts.
+EXL3_HD constexpr inline int cost_row_tree_bits(int K) {
+  return K == 2 ? 2 : (K == 3 ? 1 : (K == 4 ? 2 : (K == 5 ? 5 : 0)));
+}
 EXL3_HD inline uint32_t cost_row_pos(int K, uint32_t x) {
-  if (K == 2)
-    return (x >> 12) | (((x >> 10) & 3u) << 2) | (((x >> 1) & 511u) << 4) | ((x & 1u) << 13);
   const int ks = 16 - 2 * K;
-  return ((x & ((1u << ks) - 1u)) << K) | (x >> ks);
+  const int a = cost_row_tree_bits(K);
+  if (a == 0) return ((x & ((1u << ks) - 1u)) << K) | (x >> ks);
+  const int kb = 16 - K, lo = ks - K;
+  const uint32_t rest = ((x >> 1) & ((1u << (lo - 1)) - 1u)) |
+                        (((x >> (lo + a)) & ((1u << (ks - lo - a)) - 1u)) << (lo - 1));
+  return (x >> ks) | (((x >> lo) & ((1u << a) - 1u)) << K) | (rest << (K + a)) |
+         ((x & 1u) << (kb - 1));
 }
 // The edge at position t of a stored row (the inverse of cost_row_pos).
 EXL3_HD inline uint32_t cost_row_edge(int K, uint32_t t) {
-  if (K == 2)
-    return ((t & 3u) << 12) | (((t >> 2) & 3u) << 10) | (((t >> 4) & 511u) << 1) | (t >> 13);
   const int ks = 16 - 2 * K;
-  return ((t & ((1u << K) - 1u)) << ks) | (t >> K);
+  const int a = cost_row_tree_bits(K);
+  if (a == 0) return ((t & ((1u << K) - 1u)) << ks) | (t >> K);
+  const int kb = 16 - K, lo = ks - K;
+  const uint32_t rest = (t >> (K + a)) & ((1u << (ks - 1 - a)) - 1u);
+  return ((t & ((1u << K) - 1u)) << ks) | (((t >> K) & ((1u << a) - 1u)) << lo) |
+         ((rest & ((1u << (lo - 1)) - 1u)) << 1) | ((rest >> (lo - 1)) << (lo + a)) |
+         (t >> (kb - 1));
 }
 // First row the pass-1 traceback reaches: it covers steps L-1 .. L/2 and
 // needs the stored row at or before L/2 - 1.

@@ -65,7 +65,7 @@ def test_backpointer_slots_are_a_permutation(K):
     assert lib.exl3_backpointer_slot(K, E) == -1
 
 
-@pytest.mark.parametrize("K", [1, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("K", [1, 6, 7])
 def test_cost_row_positions_are_group_major(K):
     """Cost rows hold predecessor edge x = (k << (16-2K)) | h at (h << K) | k."""
     lib = _native.load_library()
@@ -83,27 +83,30 @@ def _predecessors(edges, K):
     return ((k[None, :] << (16 - K)) | np.asarray(edges)[:, None]).reshape(-1) >> K
 
 
-def test_k2_cost_rows_keep_traceback_trees_together():
-    """K = 2 stores every fourth step; the traceback reads, per stored row,
-    the 256 costs four predecessor steps below one edge. The row layout puts
-    them in 16 aligned runs of 16 positions, each edge's 4 predecessors in
-    one aligned run in branch order, and the LDS neighbours x, x + 1 (x even)
-    at positions t and t + 8192 (the forward pass stores both from one read)."""
+@pytest.mark.parametrize("K,stride,run", [(2, 4, 16), (3, 2, 16), (4, 2, 64), (5, 2, 1024)])
+def test_cost_rows_keep_traceback_trees_together(K, stride, run):
+    """A stored row serves `stride` steps; the traceback reads, per stored
+    row, the 2^(K stride) costs `stride` predecessor steps below one edge.
+    The row layout keeps each edge's 2^K predecessors in one aligned run in
+    branch order and a whole tree in aligned runs of `run` positions, and
+    puts the LDS neighbours x, x + 1 (x even) at positions t and t + E/2
+    (the forward pass stores both from one dword read)."""
     lib = _native.load_library()
-    E = 1 << 14
-    pos = np.array([lib.exl3_backpointer_slot(2, x) for x in range(E)])
+    E = 65536 >> K
+    pos = np.array([lib.exl3_backpointer_slot(K, x) for x in range(E)])
     assert np.array_equal(np.sort(pos), np.arange(E))
     edge_at = np.argsort(pos)
-    assert np.array_equal(edge_at[8192:], edge_at[:8192] + 1) and not (edge_at[:8192] & 1).any()
-    rng = np.random.default_rng(2)
-    for e in rng.integers(0, E, size=64):
-        sib = pos[_predecessors([e], 2)]
-        assert sib[0] % 4 == 0 and np.array_equal(sib, sib[0] + np.arange(4))
+    assert np.array_equal(edge_at[E // 2:], edge_at[:E // 2] + 1)
+    assert not (edge_at[:E // 2] & 1).any()
+    rng = np.random.default_rng(K)
+    for e in rng.integers(0, E, size=32):
+        sib = pos[_predecessors([e], K)]
+        assert sib[0] % (1 << K) == 0 and np.array_equal(sib, sib[0] + np.arange(1 << K))
         leaves = [int(e)]
-        for _ in range(4):
-            leaves = _predecessors(leaves, 2)
-        p = np.sort(pos[leaves]).reshape(16, 16)
-        assert (p[:, 0] % 16 == 0).all() and (p == p[:, :1] + np.arange(16)).all()
+        for _ in range(stride):
+            leaves = _predecessors(leaves, K)
+        p = np.sort(pos[leaves]).reshape(-1, run)
+        assert (p[:, 0] % run == 0).all() and (p == p[:, :1] + np.arange(run)).all()
 
 
 @pytest.mark.parametrize("K,cb,L,msg", [
