@@ -291,12 +291,17 @@ struct RowGather {
                                       (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
     if constexpr (exl3::cost_row_tree_bits(K) > 0 && PAD == 0 && W == 8) {
       // Positions t and t + E/2 hold the LDS neighbours x and x + 1 (x
-      // even): thread c < E/16 takes pieces c and c + E/16 from eight dword
-      // reads, their halves sorted into the two pieces by v_perm.
+      // even): the first E/16 threads take pieces c and c + E/16 each, from
+      // eight dword reads, their halves sorted into the two pieces by
+      // v_perm. Lane l of a wave takes piece 2 (l mod 32) + l / 32 of the
+      // wave's 64: piece bit 0 selects a far LDS bank row, so each half-wave
+      // reads 32 different banks, and the wave's store is still one
+      // contiguous kilobyte.
       constexpr int HALF = PIECES / 2;
-      static_assert(HALF <= NT, "one pair of pieces per thread");
-      const int c = threadIdx.x;
-      if (HALF == NT || c < HALF) {
+      static_assert(HALF <= NT && HALF % 64 == 0, "one pair of pieces per thread");
+      const int tid = threadIdx.x;
+      const int c = (tid & ~63) | ((tid & 31) << 1) | ((tid >> 5) & 1);
+      if (HALF == NT || tid < HALF) {
         const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
         uint32_t r[8];
 #pragma unroll
