@@ -117,6 +117,15 @@ def _check_device_tensor(t, name: str, dtype, ndim: int) -> int:
     return t.device.index if t.device.index is not None else torch.cuda.current_device()
 
 
+def _check_buffer(t, name: str, dtype, shape, dev: int) -> None:
+    """A device tensor of exactly ``shape`` on device ``dev``: every buffer a
+    kernel indexes by the launch's sizes is checked before the launch."""
+    if _check_device_tensor(t, name, dtype, len(shape)) != dev:
+        raise RuntimeError(f"{name} must be on the same GPU device")
+    if tuple(t.shape) != tuple(shape):
+        raise RuntimeError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
 def _resolve_cb(mcg: bool, mul1: bool) -> int:
     """quantize_xpu.cpp:85-91."""
     if mcg and mul1:
@@ -361,10 +370,8 @@ class QuantizeExtension:
         ``nan_count`` (device int32, one element) gains one per NaN value."""
         torch = _torch()
         dev = _check_device_tensor(raw, "raw", torch.float32, 2)
-        _check_device_tensor(out, "out", torch.float32, 2)
         n, L = raw.shape
-        if tuple(out.shape) != (n, L):
-            raise RuntimeError("out must match raw")
+        _check_buffer(out, "out", torch.float32, (n, L), dev)
         counter = None
         if nan_count is not None:
             if (not isinstance(nan_count, torch.Tensor) or nan_count.dtype != torch.int32
@@ -381,19 +388,16 @@ class QuantizeExtension:
         torch = _torch()
         dev = _check_device_tensor(x, "x", torch.float32, 2)
         n, L = x.shape
-        for t, name, dt, nd in ((out_w, "out_w", torch.float32, 2),
-                                (out_idx, "out_idx", torch.int16, 2),
-                                (path_cost, "path_cost", torch.float32, 1),
-                                (distortion, "distortion", torch.float32, 1),
-                                (recon_orig, "recon_orig", torch.int16, 2)):
-            if _check_device_tensor(t, name, dt, nd) != dev:
-                raise RuntimeError(f"{name} must be on the same GPU device")
+        for t, name, dt, shape in ((out_w, "out_w", torch.float32, (n, L)),
+                                   (out_idx, "out_idx", torch.int16, (n, L)),
+                                   (path_cost, "path_cost", torch.float32, (n,)),
+                                   (distortion, "distortion", torch.float32, (n,)),
+                                   (recon_orig, "recon_orig", torch.int16, (n, L))):
+            _check_buffer(t, name, dt, shape, dev)
         if packed is not None:
-            _check_device_tensor(packed, "packed", torch.int16, 2)
-            if tuple(packed.shape) != (n, 16 * K):
-                raise RuntimeError("packed must have shape (n, 16*K)")
+            _check_buffer(packed, "packed", torch.int16, (n, 16 * K), dev)
         if permuted:
-            _check_device_tensor(raw, "raw", torch.float32, 2)
+            _check_buffer(raw, "raw", torch.float32, (n, L), dev)
         with torch.cuda.device(dev):
             _check(self.lib.exl3_finalize_tiles(
                 x.data_ptr(), raw.data_ptr() if permuted else None, out_w.data_ptr(),
@@ -404,10 +408,10 @@ class QuantizeExtension:
     def pack_trellis(self, states, packed, K: int) -> None:
         torch = _torch()
         dev = _check_device_tensor(states, "states", torch.int16, 2)
-        _check_device_tensor(packed, "packed", torch.int16, 2)
         n = states.size(0)
-        if states.size(1) != 256 or tuple(packed.shape) != (n, 16 * K):
-            raise RuntimeError("pack_trellis expects (n, 256) states and (n, 16*K) words")
+        if states.size(1) != 256 or not 1 <= K <= 8:
+            raise RuntimeError("pack_trellis expects (n, 256) states and K in 1..8")
+        _check_buffer(packed, "packed", torch.int16, (n, 16 * K), dev)
         with torch.cuda.device(dev):
             _check(self.lib.exl3_pack_trellis(states.data_ptr(), packed.data_ptr(), n, K,
                                               _stream(dev)), "pack_trellis")
@@ -416,12 +420,10 @@ class QuantizeExtension:
         """Packed (n, 16*K) int16 tiles back to (n, 256) int16 states."""
         torch = _torch()
         dev = _check_device_tensor(packed, "packed", torch.int16, 2)
-        _check_device_tensor(states, "states", torch.int16, 2)
         n = packed.size(0)
-        if not 1 <= K <= 8 or packed.size(1) != 16 * K or tuple(states.shape) != (n, 256):
-            raise RuntimeError("unpack_trellis expects (n, 16*K) words and (n, 256) states")
-        if states.device != packed.device:
-            raise RuntimeError("states must be on the same GPU device as packed")
+        if not 1 <= K <= 8 or packed.size(1) != 16 * K:
+            raise RuntimeError("unpack_trellis expects (n, 16*K) words and K in 1..8")
+        _check_buffer(states, "states", torch.int16, (n, 256), dev)
         with torch.cuda.device(dev):
             _check(self.lib.exl3_unpack_trellis(packed.data_ptr(), states.data_ptr(), n, K,
                                                 _stream(dev)), "unpack_trellis")
@@ -430,8 +432,8 @@ class QuantizeExtension:
         """exl3_quant/xpu_probe.py ``probe_hfma`` (mode 0: fused, 1: two roundings)."""
         torch = _torch()
         dev = _check_device_tensor(dh, "dh", torch.float16, 1)
-        _check_device_tensor(cost, "cost", torch.float16, 1)
-        _check_device_tensor(out, "out", torch.float16, 1)
+        _check_buffer(cost, "cost", torch.float16, tuple(dh.shape), dev)
+        _check_buffer(out, "out", torch.float16, tuple(dh.shape), dev)
         with torch.cuda.device(dev):
             _check(self.lib.exl3_probe_hfma(dh.data_ptr(), cost.data_ptr(), out.data_ptr(),
                                             dh.numel(), int(mode), _stream(dev)), "probe_hfma")

@@ -175,11 +175,13 @@ class _PreparedModule:
     prep_seconds: float
 
 
-def _prepare_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int,
-                    tile_encoder: TileEncoder, skip_g_scale: bool,
-                    block_size: int) -> _PreparedModule:
+def _prepare_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int, cb: int,
+                    tile_encoder: TileEncoder, skip_g_scale: bool, block_size: int,
+                    ldl_cache: Optional[dict] = None) -> _PreparedModule:
     """Shape checks, regularisation (with the global-scale search unless
-    ``skip_g_scale``), Hessian rotation and block LDL (layer_quant.py:130-214)."""
+    ``skip_g_scale``), Hessian rotation and block LDL (layer_quant.py:130-214).
+    The rotation and factor depend on H alone: with ``ldl_cache``,
+    projections given the same Hessian tensor share one factorisation."""
     t0 = time.time()
     if weight.dim() != 2:
         raise ValueError(f"weight must be 2D, got shape {tuple(weight.shape)}")
@@ -197,6 +199,11 @@ def _prepare_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int,
     enc_k = getattr(tile_encoder, "K", None)
     if enc_k is not None and enc_k != K:
         raise ValueError(f"Tile encoder K={enc_k} does not match the requested K={K}.")
+    # The result (and its exported codebook marker) carries cb, so an encoder
+    # of another codebook would label its states wrongly.
+    enc_cb = getattr(tile_encoder, "cb", None)
+    if enc_cb is not None and enc_cb != cb:
+        raise ValueError(f"Tile encoder cb={enc_cb} does not match the requested cb={cb}.")
     # Global scale from the same encoder (layer_quant.py:197-203).
     g_scale_fn = None if skip_g_scale else g_scale_fn_from_encoder(tile_encoder)
 
@@ -205,11 +212,18 @@ def _prepare_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int,
     reg = regularize(weight=W, su=su, sv=sv, H_diag=H.diagonal(), skip_g_scale=skip_g_scale,
                      g_scale_fn=g_scale_fn, had_dim=HAD_DIM)
 
-    H_work = H.to(torch.float32).clone()
-    blockwise_preapply_had_l_(H_work, HAD_DIM)
-    blockwise_preapply_had_r_(H_work, HAD_DIM)
-    ldl = block_ldl(H_work, block_size=block_size)
-    fact_residual = compute_factorization_residual(H_work, ldl.cholesky)
+    key = (id(H), block_size)
+    cached = ldl_cache.get(key) if ldl_cache is not None else None
+    if cached is not None and cached[0] is H:
+        ldl, fact_residual = cached[1], cached[2]
+    else:
+        H_work = H.to(torch.float32).clone()
+        blockwise_preapply_had_l_(H_work, HAD_DIM)
+        blockwise_preapply_had_r_(H_work, HAD_DIM)
+        ldl = block_ldl(H_work, block_size=block_size)
+        fact_residual = compute_factorization_residual(H_work, ldl.cholesky)
+        if ldl_cache is not None:
+            ldl_cache[key] = (H, ldl, fact_residual)   # keeps H alive: id stays unique
     return _PreparedModule(name=name, W=W, H=H, reg=reg, ldl=ldl, fact_residual=fact_residual,
                            prep_seconds=time.time() - t0)
 
@@ -241,15 +255,20 @@ def _finish_module(pm: _PreparedModule, lq: LDLQResult, K: int, cb: int,
 def quantize_linear_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int = 2,
                            cb: int = CB_MUL1, tile_encoder: Optional[TileEncoder] = None,
                            skip_g_scale: bool = True, buf_size_k: int = DEFAULT_BUF_SIZE_K,
-                           block_size: int = DEFAULT_BLOCK_SIZE) -> QuantizedModuleResult:
+                           block_size: int = DEFAULT_BLOCK_SIZE,
+                           ldl_cache: Optional[dict] = None) -> QuantizedModuleResult:
     """Quantise one linear weight with LDLQ (layer_quant.py:130-265). The
     weight is (out, in) as in ``nn.Linear`` or already (in, out) = (k, n);
-    ``H`` is (in, in). Runs on the device of ``H``, which must be a GPU."""
+    ``H`` is (in, in). Runs on the device of ``H``, which must be a GPU. The
+    default encoder uses codebook ``cb``; a given encoder must match K and
+    cb. ``ldl_cache`` (a dict) lets calls that pass the same Hessian tensor
+    share its factorisation."""
     if H.device.type != "cuda":
         raise ValueError("quantize_linear_module runs on the GPU; move H to a cuda device")
     if tile_encoder is None:
-        tile_encoder = make_xpu_tile_encoder(K=K, device_index=H.device.index or 0)
-    pm = _prepare_module(name, weight, H, K, tile_encoder, skip_g_scale, block_size)
+        tile_encoder = make_xpu_tile_encoder(K=K, device_index=H.device.index or 0, cb=cb)
+    pm = _prepare_module(name, weight, H, K, cb, tile_encoder, skip_g_scale, block_size,
+                         ldl_cache)
     t0 = time.time()
     lq = ldlq(weight=pm.reg.weight, L=pm.ldl.transformed, encode_tiles=tile_encoder,
               buf_size_k=buf_size_k)
@@ -283,7 +302,7 @@ def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Ten
         raise ValueError("quantize_decoder_layer runs on the GPU")
     policy = memory_policy or MemoryPolicy()
     arena = ScratchArena(device_index=device.index or 0, policy=policy)
-    encoder = make_xpu_tile_encoder(K=K, device_index=device.index or 0, arena=arena)
+    encoder = make_xpu_tile_encoder(K=K, device_index=device.index or 0, arena=arena, cb=cb)
     available = {name: m for name, m in layer.named_modules()
                  if isinstance(m, torch.nn.Linear) and m.bias is None}
     selected = list(available) if module_names is None else list(module_names)
@@ -296,12 +315,16 @@ def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Ten
     torch.cuda.reset_peak_memory_stats(device)
     results: Dict[str, QuantizedModuleResult] = {}
     phases: Dict[str, float] = {}
+    # Projections of one Hessian group (q/k/v, gate/up) share one factor.
+    device_h = {id(hessians[n]): hessians[n].to(device) for n in selected}
+    ldl_cache: dict = {}
     try:
         if lockstep:
             tp = time.time()
             prepared = [_prepare_module(name, available[name].weight.data,
-                                        hessians[name].to(device), K, encoder, skip_g_scale,
-                                        block_size) for name in selected]
+                                        device_h[id(hessians[name])], K, cb, encoder,
+                                        skip_g_scale, block_size, ldl_cache)
+                        for name in selected]
             torch.cuda.synchronize(device)
             t0 = time.time()
             lqs = ldlq_lockstep([(pm.reg.weight, pm.ldl.transformed) for pm in prepared],
@@ -314,12 +337,14 @@ def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Ten
         else:
             for name in selected:
                 results[name] = quantize_linear_module(
-                    name=name, weight=available[name].weight.data, H=hessians[name].to(device),
-                    K=K, cb=cb, tile_encoder=encoder, skip_g_scale=skip_g_scale,
-                    buf_size_k=buf_size_k, block_size=block_size)
+                    name=name, weight=available[name].weight.data,
+                    H=device_h[id(hessians[name])], K=K, cb=cb, tile_encoder=encoder,
+                    skip_g_scale=skip_g_scale, buf_size_k=buf_size_k, block_size=block_size,
+                    ldl_cache=ldl_cache)
                 torch.cuda.synchronize(device)
     finally:
         arena.release()
+        ldl_cache.clear()
     tiles = sum(r.original_shape[0] * r.original_shape[1] // 256 for r in results.values())
     return LayerQuantizationReport(
         K=K, codebook="mul1" if cb == CB_MUL1 else str(cb),

@@ -157,8 +157,10 @@ def export_layer_safetensors(module_results: Dict[str, Any], output_dir: Union[s
     tensors, storage = build_layer_tensors(module_results, layer_idx=layer_idx, prefix=prefix,
                                            norm_weights=norm_weights)
     first = next(iter(module_results.values()))
+    # The file-level codebook names MCG as such, as each module's storage
+    # entry does (the reference's file level says "3inst" for it).
     meta = {"quant_format": "exl3", "producer": PRODUCER, "version": "1.0",
-            "codebook": "mul1" if first.cb == CB_MUL1 else "3inst", "bits": str(first.K)}
+            "codebook": _codebook_name(first.cb), "bits": str(first.K)}
     st_file = out / filename
     save_file({k: v.contiguous() for k, v in tensors.items()}, str(st_file), metadata=meta)
     qc_file = out / "quantization_config.json"

@@ -33,15 +33,16 @@ TileEncoder = Callable[["object"], "tuple"]
 def make_xpu_tile_encoder(K: int = 2, device_index: int = 0, arena=None, sg_size: int = 32,
                           force_global_costs: bool = False,
                           traceback_mode: str = "gpu_resident",
-                          asynchronous: bool = True) -> TileEncoder:
-    """MI355X tile encoder (``XPUTrellisEncoder``, MUL1 codebook) as an LDLQ
-    callback. The encoder and its ScratchArena are created once and reused
-    for every call (ldlq.py:352-357)."""
+                          asynchronous: bool = True, cb: int = CB_MUL1) -> TileEncoder:
+    """MI355X tile encoder (``XPUTrellisEncoder``) as an LDLQ callback. The
+    encoder and its ScratchArena are created once and reused for every call
+    (ldlq.py:352-357). ``cb`` defaults to MUL1, the reference adapter's only
+    codebook."""
     import torch
 
     from .gpu_quantizer import XPUTrellisEncoder
 
-    encoder = XPUTrellisEncoder(K=K, cb=CB_MUL1, arena=arena, device_index=device_index,
+    encoder = XPUTrellisEncoder(K=K, cb=cb, arena=arena, device_index=device_index,
                                 sg_size=sg_size, force_global_costs=force_global_costs)
     run_async = asynchronous and traceback_mode == "gpu_resident"
     state = {"nan_count": None}
@@ -73,7 +74,7 @@ def make_xpu_tile_encoder(K: int = 2, device_index: int = 0, arena=None, sg_size
         return recon, idx
 
     encode.K = K
-    encode.cb = CB_MUL1
+    encode.cb = cb
     encode.encoder = encoder
     encode.check_finite = check_finite
     return encode

@@ -102,6 +102,38 @@ def test_export_and_reload_layer(torch_mod, tmp_path):
         w_dec.numpy(), rtol=0, atol=0)
 
 
+def test_linear_module_codebook_choice(torch_mod, tmp_path):
+    """cb reaches the encoder: an MCG module's stored tensors carry the mcg
+    marker and decode with the MCG table to w_hat; an encoder of another
+    codebook is refused (its states would be labelled wrongly)."""
+    from exl3_intel_arc_quantizer_amd.layer_quant import hessian_from_activations, \
+        quantize_linear_module
+    from exl3_intel_arc_quantizer_amd.serialization import export_layer_safetensors, \
+        load_and_verify_layer_safetensors
+    from exl3_intel_arc_quantizer_amd.tile_encoder import make_xpu_tile_encoder
+    from exl3_intel_arc_quantizer_amd.trellis_format import CB_MCG, CB_MUL1
+    torch = torch_mod
+    rng = np.random.default_rng(12)
+    W = torch.from_numpy((rng.standard_normal((256, 128)) * 0.02).astype(np.float32)).cuda()
+    X = torch.from_numpy(rng.standard_normal((512, 128)).astype(np.float32)).cuda()
+    H, _ = hessian_from_activations(X)
+    res = quantize_linear_module("mlp.gate_proj", W, H, K=2, cb=CB_MCG)
+    assert res.cb == CB_MCG
+    st, _ = export_layer_safetensors({"mlp.gate_proj": res}, tmp_path, layer_idx=0)
+    from safetensors import safe_open
+    with safe_open(str(st), framework="pt") as f:
+        assert "model.layers.0.mlp.gate_proj.mcg" in set(f.keys())
+        assert f.metadata()["codebook"] == "mcg"
+    load_and_verify_layer_safetensors(st, {"mlp.gate_proj": res}, atol=5e-3)
+    enc = make_xpu_tile_encoder(K=2)
+    try:
+        with pytest.raises(ValueError, match="cb"):
+            quantize_linear_module("q", W, H, K=2, cb=CB_MCG, tile_encoder=enc)
+        assert enc.cb == CB_MUL1
+    finally:
+        enc.encoder.arena.release()
+
+
 def _hip_encoder(K):
     from exl3_intel_arc_quantizer_amd.tile_encoder import make_xpu_tile_encoder
     return make_xpu_tile_encoder(K=K)

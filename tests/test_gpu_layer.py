@@ -137,6 +137,17 @@ def test_quantize_decoder_layer_shared_arena(torch_mod):
         assert torch_mod.equal(r.encoded, seq.module_results[name].encoded), name
         assert torch_mod.equal(r.w_hat, seq.module_results[name].w_hat), name
         assert r.metrics.encoder_calls == k // 16 and r.metrics.encoder_seconds > 0
+    # One factorisation per Hessian group, equal to a module's own.
+    res = rep.module_results
+    assert res["self_attn.k_proj"].ldl_result is res["self_attn.q_proj"].ldl_result
+    assert res["mlp.up_proj"].ldl_result is res["mlp.gate_proj"].ldl_result
+    assert res["self_attn.o_proj"].ldl_result is not res["self_attn.q_proj"].ldl_result
+    from exl3_intel_arc_quantizer_amd.layer_quant import quantize_linear_module
+    alone = quantize_linear_module("self_attn.v_proj", layer.self_attn.v_proj.weight.data,
+                                   hess["self_attn.v_proj"], K=3)
+    assert torch_mod.equal(alone.encoded, res["self_attn.v_proj"].encoded)
+    assert torch_mod.equal(alone.ldl_result.transformed,
+                           res["self_attn.v_proj"].ldl_result.transformed)
 
 
 def test_ldlq_async_encoder_timing_and_nan(torch_mod):

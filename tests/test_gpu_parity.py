@@ -417,6 +417,40 @@ def test_extension_rejects_malformed_tensors(ext, torch_mod):
         ext.quantize_tiles(in_t, out_w, out_i.float(), costs, edges, 2, False, True)
 
 
+def test_helper_wrappers_reject_short_buffers(ext, torch_mod):
+    """The device-side helpers check every buffer the kernel indexes by the
+    launch's sizes (shape and device) and raise before launching."""
+    torch = torch_mod
+    dev = "cuda"
+    n, L, K = 4, 256, 3
+    x = torch.zeros((n, L), dtype=torch.float32, device=dev)
+    i16 = lambda *s: torch.zeros(s, dtype=torch.int16, device=dev)  # noqa: E731
+    f32 = lambda *s: torch.zeros(s, dtype=torch.float32, device=dev)  # noqa: E731
+    with pytest.raises(RuntimeError, match="out"):
+        ext.prepare_tiles(x, f32(n - 1, L), False)
+    good = dict(out_w=f32(n, L), out_idx=i16(n, L), packed=i16(n, 16 * K), path_cost=f32(n),
+                distortion=f32(n), recon_orig=i16(n, L))
+    for name, bad in (("path_cost", f32(n - 1)), ("distortion", f32(1)),
+                      ("recon_orig", i16(n, L - 1)), ("out_w", f32(n - 1, L)),
+                      ("packed", i16(n, 16 * K - 1))):
+        args = dict(good, **{name: bad})
+        with pytest.raises(RuntimeError, match=name):
+            ext.finalize_tiles(x, x, args["out_w"], args["out_idx"], args["packed"],
+                               args["path_cost"], args["distortion"], args["recon_orig"], K,
+                               False)
+    with pytest.raises(RuntimeError, match="raw"):
+        ext.finalize_tiles(x, f32(n - 1, L), *[good[k] for k in (
+            "out_w", "out_idx", "packed", "path_cost", "distortion", "recon_orig")], K, True)
+    with pytest.raises(RuntimeError, match="packed"):
+        ext.pack_trellis(i16(n, 256), i16(n - 1, 16 * K), K)
+    with pytest.raises(RuntimeError, match="states"):
+        ext.unpack_trellis(i16(n, 16 * K), i16(n, 255), K)
+    h = torch.zeros(8, dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError, match="out"):
+        ext.probe_hfma(h, h, h[:7], 0)
+    torch.cuda.synchronize()
+
+
 def test_config2_subsample_vs_c_oracle(torch_mod):
     """Config 2: a 1024x1024 N(0,1) fp16 matrix, tiles formed as ldlq.py:276-281
     (16-row blocks, tensor-core permuted), K=4; every 32nd tile bit-exact."""
