@@ -44,11 +44,17 @@ _SIGNATURES = {
     "exl3_pack_trellis": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
     "exl3_unpack_trellis": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
     "exl3_probe_hfma": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
+    # include/exl3_layer.h
+    "exl3_hadamard128": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_vp]),
+    "exl3_block_rms": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
+    "exl3_cholesky_diag_block": (_c_int, [_c_vp, _c_i64, _c_int, _c_i64, _c_vp, _c_vp]),
+    "exl3_cholesky_block_order": (_c_int, []),
 }
 
 
 def exported_symbols() -> list:
-    """C-ABI entry points declared in include/exl3_encoder.h."""
+    """C-ABI entry points declared in include/exl3_encoder.h and
+    include/exl3_layer.h."""
     return sorted(_SIGNATURES)
 
 
@@ -437,6 +443,66 @@ class QuantizeExtension:
         with torch.cuda.device(dev):
             _check(self.lib.exl3_probe_hfma(dh.data_ptr(), cost.data_ptr(), out.data_ptr(),
                                             dh.numel(), int(mode), _stream(dev)), "probe_hfma")
+
+
+# ------------------------------------------------- layer pipeline kernels
+
+def _matrix(t, name: str) -> int:
+    """A contiguous 2-D float32 GPU tensor; returns its device index."""
+    return _check_device_tensor(t, name, _torch().float32, 2)
+
+
+def hadamard128(x, out, side: int) -> None:
+    """``out = H @ x`` per 128-row block (side 0) or ``x @ H`` per 128-column
+    block (side 1), H the orthonormal Sylvester matrix of order 128
+    (hadamard.py:73-96); ``out`` may be ``x``."""
+    dev = _matrix(x, "x")
+    _check_buffer(out, "out", x.dtype, tuple(x.shape), dev)
+    rows, cols = x.shape
+    torch = _torch()
+    with torch.cuda.device(dev):
+        _check(load_library().exl3_hadamard128(x.data_ptr(), out.data_ptr(), rows, cols,
+                                               int(side), _stream(dev)), "hadamard128")
+
+
+def block_rms(x, out, dim: int, blocksize: int = 32) -> None:
+    """regularize.py:41-56 into ``out`` (``x.shape[1 - dim]`` elements,
+    any shape)."""
+    dev = _matrix(x, "x")
+    rows, cols = x.shape
+    n_out = cols if dim == 0 else rows
+    torch = _torch()
+    if (not isinstance(out, torch.Tensor) or out.dtype != torch.float32 or not out.is_contiguous()
+            or out.device != x.device or out.numel() != n_out):
+        raise RuntimeError(f"out must be a contiguous float32 tensor of {n_out} elements on "
+                           f"{x.device}")
+    with torch.cuda.device(dev):
+        _check(load_library().exl3_block_rms(x.data_ptr(), out.data_ptr(), rows, cols, int(dim),
+                                             int(blocksize), _stream(dev)), "block_rms")
+
+
+def cholesky_block_order() -> int:
+    return int(load_library().exl3_cholesky_block_order())
+
+
+def cholesky_diag_block(a, j0: int, nb: int, info) -> None:
+    """Factor the diagonal block ``a[j0:j0+nb, j0:j0+nb]`` of the square
+    matrix ``a`` in place; a failed pivot k records ``j0 + k + 1`` in
+    ``info`` (one int32 on the same device) unless it is already set."""
+    torch = _torch()
+    dev = _matrix(a, "a")
+    n = a.shape[0]
+    if a.shape[1] != n:
+        raise RuntimeError(f"a must be square, got {tuple(a.shape)}")
+    if not (0 <= j0 and 1 <= nb <= cholesky_block_order() and j0 + nb <= n):
+        raise RuntimeError(f"block [{j0}, {j0 + nb}) does not fit a {n} x {n} matrix")
+    if (not isinstance(info, torch.Tensor) or info.dtype != torch.int32
+            or info.device != a.device or info.numel() < 1):
+        raise RuntimeError("info must be an int32 tensor on a's device")
+    with torch.cuda.device(dev):
+        _check(load_library().exl3_cholesky_diag_block(a.data_ptr() + 4 * (j0 * n + j0), n, nb,
+                                                       j0, info.data_ptr(), _stream(dev)),
+               "cholesky_diag_block")
 
 
 _EXT: Optional[QuantizeExtension] = None

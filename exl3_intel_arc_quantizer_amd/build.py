@@ -17,8 +17,9 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
-SOURCES = [CSRC / "exl3_encoder.hip"]
-HEADERS = [CSRC / "exl3_layout.h", REPO_ROOT / "include" / "exl3_encoder.h"]
+SOURCES = [CSRC / "exl3_encoder.hip", CSRC / "exl3_layer.hip"]
+HEADERS = [CSRC / "exl3_layout.h", CSRC / "exl3_errors.h", REPO_ROOT / "include" / "exl3_encoder.h",
+           REPO_ROOT / "include" / "exl3_layer.h"]
 LIB_PATH = PKG_DIR / "libexl3_hip.so"
 OFFLOAD_ARCH = os.environ.get("EXL3_OFFLOAD_ARCH", "gfx950")
 

@@ -54,6 +54,7 @@
 #include <string>
 
 #include "../../include/exl3_encoder.h"
+#include "exl3_errors.h"
 #include "exl3_layout.h"
 
 using exl3::BpLayout;
@@ -65,33 +66,10 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------------ errors
 
-static thread_local std::string g_last_error;
-
-static int set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
-static int set_error(const char* fmt, ...) {
-  char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
-  g_last_error = buf;
-  return 1;
-}
-
-static int check_launch(const char* what) {
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return set_error("%s: launch failed: %s", what, hipGetErrorString(e));
-  return 0;
-}
-
-// Blocks of `block` threads covering `total` elements of a 1-D launch, or
-// an error when that exceeds the grid limit.
-static int grid_1d(int64_t total, int block, unsigned* blocks, const char* what) {
-  const int64_t b = (total + block - 1) / block;
-  if (total <= 0 || b > (int64_t)INT32_MAX) return set_error("%s: batch too large", what);
-  *blocks = (unsigned)b;
-  return 0;
-}
+using exl3::check_launch;
+using exl3::g_last_error;
+using exl3::grid_1d;
+using exl3::set_error;
 
 // --------------------------------------------------------------- codebook
 

@@ -1,0 +1,288 @@
+// MI355X (gfx950) kernels of the layer pipeline around the trellis encoder
+// (reference: exl3_quant/hadamard.py, regularize.py, ldlq.py):
+//
+//   had128_right_kernel / had128_left_kernel
+//       the blockwise orthonormal Sylvester transform of order 128 as a fast
+//       Walsh-Hadamard transform: 7 butterfly levels of fp32 add/sub and one
+//       scale instead of a 128-term dot product per output. HBM-bound: one
+//       read and one write of the matrix. Right (x @ H per 128-column
+//       block): one wave per 128-element row segment, two elements per lane,
+//       levels 2..7 across lanes. Left (H @ x per 128-row block): one thread
+//       per column of a row block, the 128 values in registers; loads and
+//       stores are coalesced across the wave's 64 columns.
+//   block_rms_kernel
+//       sqrt(sum of squares / n) along one dimension, summed in slices of
+//       `blocksize` and the slice sums accumulated in slice order, one thread
+//       per output.
+//   cholesky_diag_kernel
+//       the unblocked Cholesky factorisation of one diagonal block (order
+//       <= 128) inside a blocked factorisation whose panel updates and
+//       triangular solves are GEMM-class library calls: 256 threads each
+//       hold an 8x8 sub-block of the lower triangle in registers; column k
+//       is published through a double-buffered LDS vector, one barrier per
+//       column.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "../../include/exl3_layer.h"
+#include "exl3_errors.h"
+
+using exl3::check_launch;
+using exl3::set_error;
+
+namespace {
+
+// 1 / sqrt(128), rounded to fp32.
+constexpr float kHadScale = 0.088388347648318440550f;
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------- Hadamard
+
+constexpr int HAD_N = 128;
+constexpr int HAD_RIGHT_WAVES = 4;
+
+// Butterfly of lane distance h: the lane without bit h holds the lower
+// element a of each pair (a, b) and keeps a + b, its partner keeps a - b.
+__device__ __forceinline__ float had_level(float v, int lane, int h) {
+  const float p = __shfl_xor(v, h, 64);
+  return (lane & h) ? p - v : v + p;
+}
+
+__global__ void __launch_bounds__(64 * HAD_RIGHT_WAVES)
+    had128_right_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t segments) {
+  const int lane = threadIdx.x & 63;
+  const int64_t stride = (int64_t)gridDim.x * HAD_RIGHT_WAVES;
+  for (int64_t seg = (int64_t)blockIdx.x * HAD_RIGHT_WAVES + (threadIdx.x >> 6); seg < segments;
+       seg += stride) {
+    // Lane l holds elements 2l and 2l + 1 of the segment.
+    const float2 v = reinterpret_cast<const float2*>(in + seg * HAD_N)[lane];
+    float lo = v.x + v.y, hi = v.x - v.y;
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+      lo = had_level(lo, lane, h);
+      hi = had_level(hi, lane, h);
+    }
+    reinterpret_cast<float2*>(out + seg * HAD_N)[lane] = make_float2(lo * kHadScale,
+                                                                     hi * kHadScale);
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    had128_left_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  const int64_t base = (int64_t)blockIdx.y * HAD_N * cols + c;
+  float v[HAD_N];
+#pragma unroll
+  for (int r = 0; r < HAD_N; ++r) v[r] = in[base + r * cols];
+#pragma unroll
+  for (int h = 1; h < HAD_N; h <<= 1) {
+#pragma unroll
+    for (int i = 0; i < HAD_N; ++i) {
+      if (!(i & h)) {
+        const float a = v[i], b = v[i + h];
+        v[i] = a + b;
+        v[i + h] = a - b;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < HAD_N; ++r) out[base + r * cols] = v[r] * kHadScale;
+}
+
+// --------------------------------------------------------------- block RMS
+
+// Output o reduces x[o * so + t * st] over t < n.
+__global__ void __launch_bounds__(256)
+    block_rms_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t outputs,
+                     int64_t n, int64_t so, int64_t st, int blocksize) {
+  const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (o >= outputs) return;
+  const float* p = x + o * so;
+  float acc = 0.0f;
+  for (int64_t s = 0; s < n; s += blocksize) {
+    const int64_t e = s + blocksize < n ? s + blocksize : n;
+    float slice = 0.0f;
+    for (int64_t t = s; t < e; ++t) {
+      const float v = p[t * st];
+      const float sq = v * v;
+      slice = slice + sq;
+    }
+    acc = (s == 0) ? slice : acc + slice;
+  }
+  out[o] = sqrtf(acc / (float)n);
+}
+
+// -------------------------------------------------------- Cholesky block
+
+constexpr int CH_NB = 128;              // largest block order
+constexpr int CH_SB = 8;                // rows / columns of a thread's sub-block
+constexpr int CH_GRID = CH_NB / CH_SB;  // 16 x 16 sub-blocks
+constexpr int CH_THREADS = CH_GRID * CH_GRID;
+
+// Factors the nb x nb block at `a` (row-major, leading dimension lda,
+// lower triangle read) in place: L on and below the diagonal, zeros above.
+// Positions past nb act as an identity block and are never stored. A pivot
+// that is not positive (or NaN) sets *info to offset + k + 1 if *info is
+// still 0; the factorisation then carries on and its result is meaningless,
+// as LAPACK's potrf leaves it.
+__global__ void __launch_bounds__(CH_THREADS)
+    cholesky_diag_kernel(float* __restrict__ a, int64_t lda, int nb, int64_t offset,
+                         int32_t* __restrict__ info) {
+  __shared__ float col[2][CH_NB];
+  const int t = threadIdx.x;
+  const int bi = t / CH_GRID, bj = t % CH_GRID;
+  const bool active = bj <= bi;
+  const int i0 = bi * CH_SB, j0 = bj * CH_SB;
+
+  float v[CH_SB][CH_SB];
+#pragma unroll
+  for (int r = 0; r < CH_SB; ++r) {
+#pragma unroll
+    for (int c = 0; c < CH_SB; ++c) {
+      const int i = i0 + r, j = j0 + c;
+      float x = 0.0f;
+      if (i >= nb || j >= nb)
+        x = (i == j) ? 1.0f : 0.0f;
+      else if (active && j <= i)
+        x = a[(int64_t)i * lda + j];
+      v[r][c] = x;
+    }
+  }
+  if (bj == 0) {
+#pragma unroll
+    for (int r = 0; r < CH_SB; ++r) col[0][i0 + r] = v[r][0];
+  }
+  __syncthreads();
+
+  bool failed = false;
+  for (int kb = 0; kb < CH_GRID; ++kb) {
+#pragma unroll
+    for (int kc = 0; kc < CH_SB; ++kc) {
+      const int k = kb * CH_SB + kc;
+      const float* ck = col[k & 1];
+      const float d = ck[k];
+      if (t == 0 && !failed && !(d > 0.0f)) {
+        failed = true;
+        atomicCAS(info, 0, (int32_t)(offset + k + 1));
+      }
+      const float s = sqrtf(d);
+      const float rs = 1.0f / s;
+      // Column k is final: its owners store it (L[k][k] = s, below it the
+      // published column times 1/s, the scaling of LAPACK's potf2).
+      if (active && bj == kb && k < nb) {
+#pragma unroll
+        for (int r = 0; r < CH_SB; ++r) {
+          const int i = i0 + r;
+          if (i >= k && i < nb) a[(int64_t)i * lda + k] = (i == k) ? s : ck[i] * rs;
+        }
+      }
+      // Rank-1 update of the trailing lower triangle.
+      if (active && j0 + CH_SB - 1 > k) {
+        float li[CH_SB], lj[CH_SB];
+#pragma unroll
+        for (int r = 0; r < CH_SB; ++r) li[r] = ck[i0 + r] * rs;
+#pragma unroll
+        for (int c = 0; c < CH_SB; ++c) lj[c] = ck[j0 + c] * rs;
+#pragma unroll
+        for (int r = 0; r < CH_SB; ++r) {
+#pragma unroll
+          for (int c = 0; c < CH_SB; ++c) {
+            const int i = i0 + r, j = j0 + c;
+            if (j > k && i >= j) v[r][c] = fmaf(-li[r], lj[c], v[r][c]);
+          }
+        }
+      }
+      // Publish column k + 1 (rows k + 1 and below) for the next step.
+      if (k + 1 < CH_NB) {
+        const int nkb = (kc == CH_SB - 1) ? kb + 1 : kb;
+        if (active && bj == nkb) {
+#pragma unroll
+          for (int r = 0; r < CH_SB; ++r) {
+            const int i = i0 + r;
+            if (i >= k + 1) col[(k + 1) & 1][i] = v[r][(kc + 1) % CH_SB];
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // Zeros above the diagonal.
+#pragma unroll
+  for (int r = 0; r < CH_SB; ++r) {
+#pragma unroll
+    for (int c = 0; c < CH_SB; ++c) {
+      const int i = i0 + r, j = j0 + c;
+      if (j > i && i < nb && j < nb) a[(int64_t)i * lda + j] = 0.0f;
+    }
+  }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------- C-ABI
+
+extern "C" {
+
+int exl3_hadamard128(const float* in, float* out, int64_t rows, int64_t cols, int side,
+                     void* stream) {
+  if (!in || !out) return set_error("hadamard128: NULL buffer");
+  if (rows <= 0 || cols <= 0) return set_error("hadamard128: empty matrix (%lld x %lld)",
+                                                (long long)rows, (long long)cols);
+  if (side != 0 && side != 1) return set_error("hadamard128: side must be 0 or 1, got %d", side);
+  if (side == 0 && rows % HAD_N)
+    return set_error("hadamard128: rows (%lld) must be divisible by 128", (long long)rows);
+  if (side == 1 && cols % HAD_N)
+    return set_error("hadamard128: columns (%lld) must be divisible by 128", (long long)cols);
+  hipStream_t st = as_stream(stream);
+  if (side == 1) {
+    const int64_t segments = rows * (cols / HAD_N);
+    const int64_t want = (segments + HAD_RIGHT_WAVES - 1) / HAD_RIGHT_WAVES;
+    // Grid-stride beyond 65536 workgroups (several segments per wave).
+    const int64_t blocks = want < 65536 ? want : 65536;
+    if (blocks > INT32_MAX) return set_error("hadamard128: matrix too large");
+    hipLaunchKernelGGL(had128_right_kernel, dim3((unsigned)blocks), dim3(64 * HAD_RIGHT_WAVES), 0,
+                       st, in, out, segments);
+  } else {
+    const int64_t gx = (cols + 255) / 256, gy = rows / HAD_N;
+    if (gx > INT32_MAX || gy > 65535) return set_error("hadamard128: matrix too large");
+    hipLaunchKernelGGL(had128_left_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, st, in,
+                       out, cols);
+  }
+  return check_launch("hadamard128");
+}
+
+int exl3_block_rms(const float* x, float* out, int64_t rows, int64_t cols, int dim, int blocksize,
+                   void* stream) {
+  if (!x || !out) return set_error("block_rms: NULL buffer");
+  if (rows <= 0 || cols <= 0) return set_error("block_rms: empty matrix");
+  if (dim != 0 && dim != 1) return set_error("block_rms: dim must be 0 or 1, got %d", dim);
+  if (blocksize <= 0) return set_error("block_rms: blocksize must be positive, got %d", blocksize);
+  const int64_t outputs = dim == 0 ? cols : rows;
+  const int64_t n = dim == 0 ? rows : cols;
+  const int64_t so = dim == 0 ? 1 : cols, st = dim == 0 ? cols : 1;
+  unsigned blocks;
+  if (exl3::grid_1d(outputs, 256, &blocks, "block_rms")) return 1;
+  hipLaunchKernelGGL(block_rms_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), x, out,
+                     outputs, n, so, st, blocksize);
+  return check_launch("block_rms");
+}
+
+int exl3_cholesky_diag_block(float* a, int64_t lda, int nb, int64_t offset, int32_t* info,
+                             void* stream) {
+  if (!a || !info) return set_error("cholesky_diag_block: NULL buffer");
+  if (nb < 1 || nb > CH_NB)
+    return set_error("cholesky_diag_block: block order must be in 1..%d, got %d", CH_NB, nb);
+  if (lda < nb) return set_error("cholesky_diag_block: lda (%lld) < block order (%d)",
+                                 (long long)lda, nb);
+  if (offset < 0) return set_error("cholesky_diag_block: negative offset");
+  hipLaunchKernelGGL(cholesky_diag_kernel, dim3(1), dim3(CH_THREADS), 0, as_stream(stream), a, lda,
+                     nb, offset, info);
+  return check_launch("cholesky_diag_block");
+}
+
+int exl3_cholesky_block_order(void) { return CH_NB; }
+
+}  // extern "C"

@@ -6,8 +6,11 @@ from the left (``H @ x``), ``preapply_had_r`` each 128-column block from the
 right (``x @ H``). The matrix is symmetric and its own inverse, so decoding
 applies the same transforms in reverse order (``weight_from_quantized``).
 
-On the GPU every block product of a call is one batched fp32 GEMM
-(hipBLASLt through torch) instead of a Python loop over blocks.
+On the GPU the transforms are one launch of a fast Walsh-Hadamard kernel
+(``exl3_hadamard128``, HIP): 7 butterfly levels of fp32 additions and one
+scale per element instead of a 128-term product, bound by one HBM read and
+write of the matrix. The results equal the matrix products up to fp32
+rounding of the summation order.
 """
 
 from __future__ import annotations
@@ -46,40 +49,59 @@ def hadamard(n: int = HAD_DIM, dtype: torch.dtype = torch.float32,
     return cached
 
 
-def preapply_had_l(x: torch.Tensor, had_dim: int = HAD_DIM) -> torch.Tensor:
-    """H @ x on each 128-row block (hadamard.py:73-83)."""
+def _had128(x: torch.Tensor, side: int, had_dim: int, out: Optional[torch.Tensor]) -> torch.Tensor:
+    """The blockwise transform through the HIP fast Walsh-Hadamard kernel
+    (``exl3_hadamard128``); GPU tensors only."""
+    if had_dim != HAD_DIM:
+        raise ValueError(f"only had_dim={HAD_DIM} is supported, got {had_dim}")
+    if x.dim() != 2:
+        raise ValueError(f"expected a 2-D tensor, got shape {tuple(x.shape)}")
     k, n = x.shape
-    if k % had_dim != 0:
+    if side == 0 and k % had_dim != 0:
         raise ValueError(f"rows ({k}) must be divisible by had_dim ({had_dim})")
-    work = x.to(torch.float32).contiguous()
-    had = hadamard(had_dim, torch.float32, device=x.device)
-    return torch.matmul(had, work.view(-1, had_dim, n)).view(k, n).to(x.dtype)
+    if side == 1 and n % had_dim != 0:
+        raise ValueError(f"columns ({n}) must be divisible by had_dim ({had_dim})")
+    if x.device.type != "cuda":
+        raise ValueError("the Hadamard transforms run on the GPU; move the tensor to a cuda device")
+    from ._native import hadamard128
+    work = x if (x.dtype == torch.float32 and x.is_contiguous()) else \
+        x.to(torch.float32).contiguous()
+    if out is None:
+        out = torch.empty_like(work)
+    hadamard128(work, out, side)
+    return out
+
+
+def preapply_had_l(x: torch.Tensor, had_dim: int = HAD_DIM) -> torch.Tensor:
+    """H @ x on each 128-row block (hadamard.py:73-83), as a new tensor of
+    x's dtype."""
+    return _had128(x, 0, had_dim, None).to(x.dtype)
 
 
 def preapply_had_r(x: torch.Tensor, had_dim: int = HAD_DIM) -> torch.Tensor:
-    """x @ H on each 128-column block (hadamard.py:86-96)."""
-    k, n = x.shape
-    if n % had_dim != 0:
-        raise ValueError(f"columns ({n}) must be divisible by had_dim ({had_dim})")
-    work = x.to(torch.float32).contiguous()
-    had = hadamard(had_dim, torch.float32, device=x.device)
-    return torch.matmul(work.view(k, -1, had_dim), had).view(k, n).to(x.dtype)
+    """x @ H on each 128-column block (hadamard.py:86-96), as a new tensor of
+    x's dtype."""
+    return _had128(x, 1, had_dim, None).to(x.dtype)
+
+
+def _in_place(x: torch.Tensor, side: int, had_dim: int) -> torch.Tensor:
+    if x.dtype != torch.float32:
+        raise ValueError(f"in-place Hadamard requires float32, got {x.dtype}")
+    if x.is_contiguous():
+        _had128(x, side, had_dim, x)
+    else:
+        x.copy_(_had128(x, side, had_dim, None))
+    return x
 
 
 def blockwise_preapply_had_l_(x: torch.Tensor, had_dim: int = HAD_DIM) -> torch.Tensor:
     """In-place H @ x on 128-row blocks of a float32 matrix (hadamard.py:99-111)."""
-    if x.dtype != torch.float32:
-        raise ValueError(f"in-place Hadamard requires float32, got {x.dtype}")
-    x.copy_(preapply_had_l(x, had_dim))
-    return x
+    return _in_place(x, 0, had_dim)
 
 
 def blockwise_preapply_had_r_(x: torch.Tensor, had_dim: int = HAD_DIM) -> torch.Tensor:
     """In-place x @ H on 128-column blocks of a float32 matrix (hadamard.py:114-126)."""
-    if x.dtype != torch.float32:
-        raise ValueError(f"in-place Hadamard requires float32, got {x.dtype}")
-    x.copy_(preapply_had_r(x, had_dim))
-    return x
+    return _in_place(x, 1, had_dim)
 
 
 def weight_from_quantized(w_hat: torch.Tensor, su: torch.Tensor,
@@ -89,7 +111,7 @@ def weight_from_quantized(w_hat: torch.Tensor, su: torch.Tensor,
     k, n = w_hat.shape
     if su.numel() != k or sv.numel() != n:
         raise ValueError(f"su must have {k} elements and sv {n}, got {su.numel()} / {sv.numel()}")
-    work = preapply_had_l(w_hat.to(torch.float32), HAD_DIM)
-    work = work * su.to(torch.float32).reshape(k, 1)
-    work = preapply_had_r(work, HAD_DIM)
-    return work * sv.to(torch.float32).reshape(1, n)
+    work = _had128(w_hat, 0, HAD_DIM, None)          # a new tensor: w_hat is not modified
+    work.mul_(su.to(device=work.device, dtype=torch.float32).reshape(k, 1))
+    _had128(work, 1, HAD_DIM, work)
+    return work.mul_(sv.to(device=work.device, dtype=torch.float32).reshape(1, n))

@@ -1,10 +1,11 @@
 """Block LDL factorisation and the LDLQ error-feedback traversal on the GPU
 (reference: exl3_quant/ldlq.py).
 
-``block_ldl`` factors the (Hadamard-rotated, damped) Hessian H = L L^T with
-rocSOLVER (``torch.linalg.cholesky``), inverts every 16x16 diagonal block in
-one batched call and folds the inverses into their block columns with one
-batched GEMM; the diagonal blocks become identities.
+``block_ldl`` factors the (Hadamard-rotated, damped) Hessian H = L L^T with a
+blocked Cholesky (``cholesky_ex``: diagonal blocks factored by a HIP kernel,
+panel updates and solves as GEMM-class library calls), inverts every 16x16
+diagonal block in one batched call and folds the inverses into their block
+columns with one batched GEMM; the diagonal blocks become identities.
 
 ``ldlq`` quantises a (k, n) weight bottom-up: spans of ``buf_size_k`` rows
 from the last, 16-row blocks inside a span from the last. Each block's rows
@@ -39,7 +40,7 @@ DEFAULT_MAX_RETRIES = 10
 DEFAULT_BUF_SIZE_K = 128
 
 __all__ = ["DEFAULT_BLOCK_SIZE", "DEFAULT_SIGMA_REG", "DEFAULT_MAX_RETRIES", "DEFAULT_BUF_SIZE_K",
-           "BlockLDLResult", "block_ldl", "LDLQResult", "ldlq", "ldlq_lockstep", "TileEncoder",
+           "BlockLDLResult", "cholesky_ex", "block_ldl", "LDLQResult", "ldlq", "ldlq_lockstep", "TileEncoder",
            "make_xpu_tile_encoder", "make_gpu_tile_encoder"]
 
 
@@ -56,13 +57,50 @@ class BlockLDLResult:
     block_size: int
 
 
+def cholesky_ex(A: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Lower Cholesky factor of a symmetric positive-definite float32 GPU
+    matrix and an int32 ``info``: 0, or the 1-based order of the first
+    leading minor found not positive definite (``torch.linalg.cholesky_ex``'s
+    contract; only the lower triangle of ``A`` is read, ``A`` is not
+    modified).
+
+    Left-looking and blocked by the HIP kernel's block order (128): panel j
+    gets the product of the finished columns to its left subtracted (one
+    GEMM, ``addmm_`` on the strided panel view), its diagonal block is
+    factored in LDS by ``exl3_cholesky_diag_block`` and the rows below are
+    solved against it (``solve_triangular``, a rocBLAS trsm). No host
+    synchronisation: ``info`` stays on the device."""
+    from ._native import cholesky_block_order, cholesky_diag_block
+    if A.dim() != 2 or A.shape[0] != A.shape[1] or A.dtype != torch.float32:
+        raise ValueError(f"cholesky_ex expects a square float32 matrix, got {A.dtype} "
+                         f"{tuple(A.shape)}")
+    if A.device.type != "cuda":
+        raise ValueError("cholesky_ex runs on the GPU; move the matrix to a cuda device")
+    n = A.shape[0]
+    nb = cholesky_block_order()
+    L = A.contiguous().clone()
+    info = torch.zeros(1, dtype=torch.int32, device=A.device)
+    for j0 in range(0, n, nb):
+        j1 = min(n, j0 + nb)
+        if j0 > 0:
+            L[j0:, j0:j1].addmm_(L[j0:, :j0], L[j0:j1, :j0].T, beta=1.0, alpha=-1.0)
+        cholesky_diag_block(L, j0, j1 - j0, info)
+        if j1 < n:
+            panel = L[j1:, j0:j1]
+            panel.copy_(torch.linalg.solve_triangular(L[j0:j1, j0:j1].T, panel, upper=True,
+                                                      left=False))
+    return L.tril_(), info
+
+
 def block_ldl(H: torch.Tensor, block_size: int = DEFAULT_BLOCK_SIZE,
               sigma_reg: float = DEFAULT_SIGMA_REG,
               max_retries: int = DEFAULT_MAX_RETRIES) -> BlockLDLResult:
     """Block-folded Cholesky factor consumed by :func:`ldlq` (ldlq.py:76-142).
     ``H`` is not modified; after a failed factorisation an internal copy is
     damped by 2 sigma_reg mean(diag) and factored again, up to
-    ``max_retries`` times."""
+    ``max_retries`` times. The factorisation is :func:`cholesky_ex`; the
+    diagonal 16 x 16 blocks of the factor are inverted in one batched call
+    and folded into their block columns with one batched GEMM."""
     if H.dim() != 2 or H.shape[0] != H.shape[1]:
         raise ValueError(f"H must be a square 2-D tensor, got shape {tuple(H.shape)}")
     if H.dtype != torch.float32:
@@ -76,7 +114,7 @@ def block_ldl(H: torch.Tensor, block_size: int = DEFAULT_BLOCK_SIZE,
     chol = None
     retries = 0
     for attempt in range(max_retries + 1):
-        chol, info = torch.linalg.cholesky_ex(work)
+        chol, info = cholesky_ex(work)
         if int(info.item()) == 0:
             retries = attempt
             break
@@ -85,18 +123,16 @@ def block_ldl(H: torch.Tensor, block_size: int = DEFAULT_BLOCK_SIZE,
                 f"block_ldl: Cholesky failed after {max_retries} damping steps")
         work.diagonal().add_(2.0 * sigma_reg * work.diagonal().mean())
     m = n // block_size
-    # (m, bs, bs) diagonal blocks, inverted in one batched call.
-    diag_blocks = torch.stack([chol[b * block_size:(b + 1) * block_size,
-                                    b * block_size:(b + 1) * block_size] for b in range(m)])
-    inverses = torch.linalg.inv(diag_blocks.contiguous())
+    # The m diagonal blocks as a strided view: [b, r, c] = chol[b bs + r, b bs + c].
+    diag_view = chol.view(m, block_size, m, block_size).diagonal(dim1=0, dim2=2)
+    inverses = torch.linalg.inv(diag_view.permute(2, 0, 1).contiguous())
     # Column block b of the factor times its inverse: one batched GEMM.
     cols = chol.view(n, m, block_size).permute(1, 0, 2).contiguous()      # (m, n, bs)
-    folded = torch.matmul(cols, inverses.contiguous())                      # (m, n, bs)
+    folded = torch.matmul(cols, inverses)                                  # (m, n, bs)
     transformed = folded.permute(1, 0, 2).reshape(n, n).contiguous()
     eye = torch.eye(block_size, dtype=H.dtype, device=H.device)
-    for b in range(m):
-        transformed[b * block_size:(b + 1) * block_size,
-                    b * block_size:(b + 1) * block_size] = eye
+    transformed.view(m, block_size, m, block_size).diagonal(dim1=0, dim2=2).copy_(
+        eye.unsqueeze(-1).expand(block_size, block_size, m))
     return BlockLDLResult(transformed=transformed, cholesky=chol, block_inverses=inverses,
                           retries=retries, damping_applied=retries > 0, n=n,
                           block_size=block_size)

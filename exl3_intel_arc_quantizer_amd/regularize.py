@@ -25,14 +25,26 @@ EPS = 1e-10
 
 def block_rms(x: torch.Tensor, dim: int, keepdim: bool = False,
               blocksize: int = 32) -> torch.Tensor:
-    """sqrt(mean of squares) accumulated over 32-slices in order
-    (regularize.py:41-56); the slice order fixes the rounding."""
-    n = x.size(dim)
-    sq = None
-    for block in torch.split(x, blocksize, dim=dim):
-        block_sq = block.square().sum(dim=dim, keepdim=keepdim)
-        sq = block_sq if sq is None else sq + block_sq
-    return (sq / n).sqrt()
+    """sqrt(mean of squares) along ``dim`` of a 2-D GPU tensor, the squares
+    summed in ``blocksize`` slices whose sums are accumulated in slice order
+    (regularize.py:41-56); the slice order fixes the rounding. One launch of
+    the HIP kernel ``exl3_block_rms``."""
+    if x.dim() != 2:
+        raise ValueError(f"block_rms expects a 2-D tensor, got shape {tuple(x.shape)}")
+    if x.device.type != "cuda":
+        raise ValueError("block_rms runs on the GPU; move the tensor to a cuda device")
+    from ._native import block_rms as _block_rms
+    d = dim % 2
+    rows, cols = x.shape
+    work = x if (x.dtype == torch.float32 and x.is_contiguous()) else \
+        x.to(torch.float32).contiguous()
+    if keepdim:
+        shape = (1, cols) if d == 0 else (rows, 1)
+    else:
+        shape = (cols,) if d == 0 else (rows,)
+    out = torch.empty(shape, dtype=torch.float32, device=x.device)
+    _block_rms(work, out, d, int(blocksize))
+    return out
 
 
 @dataclass

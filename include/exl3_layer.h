@@ -1,0 +1,52 @@
+/*
+ * exl3_layer.h — C-ABI of the MI355X (gfx950) kernels of the layer pipeline
+ * around the trellis encoder (alpha2beta/EXL3_Intel_Arc_quantizer's
+ * exl3_quant/hadamard.py, regularize.py and ldlq.py, which do this work with
+ * torch tensor operations). Same conventions as exl3_encoder.h: device
+ * buffers owned by the caller, nothing allocated, work enqueued on `stream`
+ * (a hipStream_t, NULL = the null stream), 0 on success and a message in
+ * exl3_last_error() otherwise. Matrices are float32, row-major, contiguous.
+ */
+#ifndef EXL3_LAYER_H
+#define EXL3_LAYER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Replaces preapply_had_l / preapply_had_r (hadamard.py:73-96) and their
+ * in-place forms (hadamard.py:99-126): the orthonormal Sylvester matrix of
+ * order 128, H[i][j] = (-1)^popcount(i & j) / sqrt(128), applied blockwise.
+ * side = 0: out = H @ in on every 128-row block (rows % 128 == 0);
+ * side = 1: out = in @ H on every 128-column block (cols % 128 == 0).
+ * Computed as a fast Walsh-Hadamard transform in fp32; in == out is allowed. */
+int exl3_hadamard128(const float* in, float* out, int64_t rows, int64_t cols, int side,
+                     void* stream);
+
+/* Replaces block_rms (regularize.py:41-56): out = sqrt(S / n), S the sum of
+ * squares along `dim` (0: over rows, one output per column; 1: over
+ * columns, one per row) taken in slices of `blocksize` whose sums are
+ * accumulated in slice order. */
+int exl3_block_rms(const float* x, float* out, int64_t rows, int64_t cols, int dim, int blocksize,
+                   void* stream);
+
+/* The diagonal-block step of a blocked Cholesky factorisation, which
+ * replaces torch.linalg.cholesky_ex in block_ldl (ldlq.py:76-142): factors
+ * the nb x nb block at `a` (leading dimension lda, lower triangle read,
+ * nb <= exl3_cholesky_block_order()) in place into L (zeros above the
+ * diagonal). A non-positive or NaN pivot k sets *info (device int32) to
+ * offset + k + 1 unless it is already non-zero. */
+int exl3_cholesky_diag_block(float* a, int64_t lda, int nb, int64_t offset, int32_t* info,
+                             void* stream);
+
+/* Largest block order exl3_cholesky_diag_block accepts (128). */
+int exl3_cholesky_block_order(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_LAYER_H */

@@ -1,0 +1,160 @@
+"""HIP kernels of the layer pipeline (include/exl3_layer.h) against float64
+numpy: the blockwise Hadamard transform (hadamard.py:73-126) against the
+Sylvester matrix product, block_rms (regularize.py:41-56) against a float64
+sum of squares, and the blocked Cholesky (cholesky_ex, the factorisation of
+block_ldl, ldlq.py:76-142) against numpy.linalg.cholesky, including the
+failure index of matrices that are not positive definite."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import ldlq_ref
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+    return torch
+
+
+def _sylvester64(n=128):
+    i = np.arange(n)
+    pop = np.vectorize(lambda v: bin(v).count("1"))(i[:, None] & i[None, :])
+    return np.where(pop % 2 == 0, 1.0, -1.0) / np.sqrt(n)
+
+
+def _blockwise_left(x, h):
+    k, n = x.shape
+    return np.einsum("ij,bjn->bin", h, x.reshape(k // 128, 128, n)).reshape(k, n)
+
+
+@pytest.mark.parametrize("shape", [(128, 128), (256, 384), (384, 1000), (1024, 128)])
+def test_hadamard128_matches_sylvester_product(torch_mod, shape):
+    torch = torch_mod
+    from exl3_intel_arc_quantizer_amd import hadamard
+    rng = np.random.default_rng(sum(shape))
+    k, n = shape
+    x = rng.standard_normal((k, n)).astype(np.float32)
+    h = _sylvester64()
+    np.testing.assert_allclose(h, ldlq_ref.hadamard(), rtol=0, atol=1e-7)
+    xt = torch.from_numpy(x).cuda()
+    want_l = _blockwise_left(x.astype(np.float64), h)
+    got_l = hadamard.preapply_had_l(xt).cpu().numpy()
+    np.testing.assert_allclose(got_l, want_l, rtol=0, atol=2e-6 * np.abs(want_l).max())
+    if n % 128 == 0:
+        want_r = _blockwise_left(x.astype(np.float64).T, h).T
+        got_r = hadamard.preapply_had_r(xt).cpu().numpy()
+        np.testing.assert_allclose(got_r, want_r, rtol=0, atol=2e-6 * np.abs(want_r).max())
+        # In place, and the transform is its own inverse.
+        y = xt.clone()
+        hadamard.blockwise_preapply_had_r_(y)
+        assert np.array_equal(y.cpu().numpy(), got_r)
+        hadamard.blockwise_preapply_had_r_(y)
+        np.testing.assert_allclose(y.cpu().numpy(), x, rtol=0, atol=1e-5)
+    else:
+        with pytest.raises(ValueError, match="divisible"):
+            hadamard.preapply_had_r(xt)
+    y = xt.clone()
+    hadamard.blockwise_preapply_had_l_(y)
+    assert np.array_equal(y.cpu().numpy(), got_l)
+    # A unit vector maps to a signed column of the matrix.
+    e = torch.zeros((128, n), device="cuda")
+    e[5, 3] = 1.0
+    col = hadamard.preapply_had_l(e).cpu().numpy()[:, 3]
+    np.testing.assert_allclose(col, h[:, 5], rtol=0, atol=1e-7)
+
+
+def test_hadamard128_rejects_bad_shapes(torch_mod):
+    torch = torch_mod
+    from exl3_intel_arc_quantizer_amd import _native
+    x = torch.zeros((100, 128), device="cuda")
+    with pytest.raises(RuntimeError, match="divisible by 128"):
+        _native.hadamard128(x, x, 0)
+    with pytest.raises(RuntimeError, match="side"):
+        _native.hadamard128(x, x, 2)
+    with pytest.raises(RuntimeError, match="shape"):
+        _native.hadamard128(x, torch.zeros((100, 64), device="cuda"), 1)
+
+
+@pytest.mark.parametrize("shape,blocksize", [((256, 384), 32), ((100, 70), 32), ((33, 1000), 7)])
+def test_block_rms_matches_float64(torch_mod, shape, blocksize):
+    torch = torch_mod
+    from exl3_intel_arc_quantizer_amd.regularize import block_rms
+    rng = np.random.default_rng(shape[0])
+    x = (rng.standard_normal(shape) * rng.uniform(0.1, 10, size=shape[1])).astype(np.float32)
+    xt = torch.from_numpy(x).cuda()
+    for dim in (0, 1):
+        want = np.sqrt((x.astype(np.float64) ** 2).mean(axis=dim))
+        got = block_rms(xt, dim=dim, keepdim=True, blocksize=blocksize)
+        assert tuple(got.shape) == ((1, shape[1]) if dim == 0 else (shape[0], 1))
+        np.testing.assert_allclose(got.cpu().numpy().ravel(), want, rtol=2e-6)
+    # Slice order: a single 32-slice equals the plain sequential sum.
+    z = torch.zeros((32, 3), device="cuda")
+    z[:, 1] = 2.0
+    np.testing.assert_array_equal(block_rms(z, dim=0).cpu().numpy(), [0.0, 2.0, 0.0])
+
+
+def _spd(n, seed, cond_shift=0.05):
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((n + 8, n))
+    X[:, rng.random(n) < 0.05] *= 10.0
+    return ((X.T @ X) / (n + 8) + cond_shift * np.eye(n)).astype(np.float32)
+
+
+@pytest.mark.parametrize("n", [1, 5, 128, 129, 300, 512])
+def test_cholesky_matches_numpy(torch_mod, n):
+    torch = torch_mod
+    from exl3_intel_arc_quantizer_amd.ldlq import cholesky_ex
+    A = _spd(n, n)
+    # Upper-triangle garbage must not be read.
+    A_in = A.copy()
+    A_in[np.triu_indices(n, 1)] = 7.0
+    L, info = cholesky_ex(torch.from_numpy(A_in).cuda())
+    assert int(info.item()) == 0
+    Lh = L.cpu().numpy()
+    assert not np.any(np.triu(Lh, 1)), "non-zero above the diagonal"
+    want = np.linalg.cholesky(A.astype(np.float64))
+    np.testing.assert_allclose(Lh, want, rtol=0, atol=5e-5 * np.abs(want).max())
+    resid = np.linalg.norm(A - Lh.astype(np.float64) @ Lh.T.astype(np.float64)) / np.linalg.norm(A)
+    assert resid < 2e-6, resid
+
+
+@pytest.mark.parametrize("n,bad", [(64, 0), (300, 2), (300, 200), (512, 511)])
+def test_cholesky_failure_index(torch_mod, n, bad):
+    """info = 1-based order of the first leading minor that is not positive
+    definite, as torch.linalg.cholesky_ex reports it."""
+    torch = torch_mod
+    from exl3_intel_arc_quantizer_amd.ldlq import cholesky_ex
+    A = np.eye(n, dtype=np.float32)
+    A[bad, bad] = -1.0
+    _, info = cholesky_ex(torch.from_numpy(A).cuda())
+    assert int(info.item()) == bad + 1
+    _, info_t = torch.linalg.cholesky_ex(torch.from_numpy(A).double())
+    assert int(info_t) == bad + 1
+    A = _spd(n, 3)
+    A[bad, bad] = float("nan")
+    _, info = cholesky_ex(torch.from_numpy(A).cuda())
+    assert int(info.item()) == bad + 1
+
+
+def test_block_ldl_damping_retries_on_gpu(torch_mod):
+    """A matrix just below positive definite fails once, is damped by
+    2 sigma mean(diag) (ldlq.py:96-104) and factors; the folded factor has
+    identity diagonal blocks and matches the numpy oracle."""
+    torch = torch_mod
+    from exl3_intel_arc_quantizer_amd.ldlq import block_ldl
+    A = _spd(256, 9).astype(np.float64)
+    w_min = np.linalg.eigvalsh(A)[0]
+    A = (A - (w_min + 1e-3) * np.eye(256)).astype(np.float32)
+    res = block_ldl(torch.from_numpy(A).cuda())
+    assert res.retries >= 1 and res.damping_applied
+    ref_T, _, ref_retries = ldlq_ref.block_ldl(A)
+    assert res.retries == ref_retries
+    T = res.transformed.cpu().numpy()
+    for b in range(16):
+        np.testing.assert_array_equal(T[16 * b:16 * b + 16, 16 * b:16 * b + 16], np.eye(16))
+    np.testing.assert_allclose(T, ref_T, rtol=0, atol=5e-4 * np.abs(ref_T).max())

@@ -14,12 +14,15 @@ from exl3_intel_arc_quantizer_amd.build import LIB_PATH
 
 from .conftest import REPO_ROOT
 
-HEADER = REPO_ROOT / "include" / "exl3_encoder.h"
+HEADERS = sorted((REPO_ROOT / "include").glob("*.h"))
 
 
 def _declared_symbols():
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(exl3_\w+)\s*\(", text, re.M)))
+    names = set()
+    for header in HEADERS:
+        text = header.read_text()
+        names |= set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(exl3_\w+)\s*\(", text, re.M))
+    return sorted(names)
 
 
 def test_library_built_in_tree():
@@ -29,9 +32,9 @@ def test_library_built_in_tree():
 def test_header_symbols_are_exported():
     lib = ctypes.CDLL(str(LIB_PATH))
     declared = _declared_symbols()
-    assert len(declared) >= 13
+    assert len(HEADERS) == 2 and len(declared) >= 17
     for name in declared:
-        assert hasattr(lib, name), f"{name} declared in exl3_encoder.h but not exported"
+        assert hasattr(lib, name), f"{name} declared in include/*.h but not exported"
     assert declared == _native.exported_symbols()
 
 
