@@ -49,6 +49,8 @@ _SIGNATURES = {
     "exl3_block_rms": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
     "exl3_cholesky_diag_block": (_c_int, [_c_vp, _c_i64, _c_int, _c_i64, _c_vp, _c_vp]),
     "exl3_cholesky_block_order": (_c_int, []),
+    "exl3_ldlq_gather": (_c_int, [_c_vp, _c_int, _c_i64, _c_vp, _c_vp]),
+    "exl3_ldlq_scatter": (_c_int, [_c_vp, _c_int, _c_i64, _c_vp, _c_vp, _c_vp]),
 }
 
 
@@ -503,6 +505,49 @@ def cholesky_diag_block(a, j0: int, nb: int, info) -> None:
         _check(load_library().exl3_cholesky_diag_block(a.data_ptr() + 4 * (j0 * n + j0), n, nb,
                                                        j0, info.data_ptr(), _stream(dev)),
                "cholesky_diag_block")
+
+
+LDLQ_BLOCK_FIELDS = ("w", "comp", "wq", "err", "states", "n", "tile0", "reserved")
+
+
+def _ldlq_table(table, tiles_like, name: str) -> tuple:
+    torch = _torch()
+    dev = _check_device_tensor(tiles_like, name, tiles_like.dtype, 2)
+    if tiles_like.size(1) != 256:
+        raise RuntimeError(f"{name} must be (tiles, 256), got {tuple(tiles_like.shape)}")
+    if (not isinstance(table, torch.Tensor) or table.dtype != torch.int64 or table.dim() != 2
+            or table.size(1) != len(LDLQ_BLOCK_FIELDS) or not table.is_contiguous()
+            or table.device != tiles_like.device or table.size(0) < 1):
+        raise RuntimeError("the block table must be a contiguous (blocks, 8) int64 tensor on "
+                           f"{tiles_like.device}")
+    return dev, table.size(0), tiles_like.size(0)
+
+
+def ldlq_gather(table, x) -> None:
+    """Tile formation of one LDLQ encoder call (exl3_ldlq_gather): ``table``
+    is the call's (blocks, 8) int64 ``exl3_ldlq_block`` rows on the device,
+    whose addresses the caller has checked; ``x`` receives (tiles, 256)
+    float32 tiles in tensor-core order."""
+    torch = _torch()
+    dev, nb, tiles = _ldlq_table(table, x, "x")
+    if x.dtype != torch.float32:
+        raise RuntimeError("x must be float32")
+    with torch.cuda.device(dev):
+        _check(load_library().exl3_ldlq_gather(table.data_ptr(), nb, tiles, x.data_ptr(),
+                                               _stream(dev)), "ldlq_gather")
+
+
+def ldlq_scatter(table, recon, idx) -> None:
+    """Write-back of one LDLQ encoder call (exl3_ldlq_scatter) from the
+    encoder's (tiles, 256) float32 reconstruction and int16 states."""
+    torch = _torch()
+    dev, nb, tiles = _ldlq_table(table, recon, "recon")
+    if recon.dtype != torch.float32:
+        raise RuntimeError("recon must be float32")
+    _check_buffer(idx, "idx", torch.int16, tuple(recon.shape), dev)
+    with torch.cuda.device(dev):
+        _check(load_library().exl3_ldlq_scatter(table.data_ptr(), nb, tiles, recon.data_ptr(),
+                                                idx.data_ptr(), _stream(dev)), "ldlq_scatter")
 
 
 _EXT: Optional[QuantizeExtension] = None

@@ -99,24 +99,8 @@ __global__ void decode_codebook_kernel(int cb, uint16_t* __restrict__ out) {
 
 // ------------------------------------------------------- tile permutation
 
-// tensor_core_perm (reference trellis_format.py:88-108): encoded element
-// 8t + s is original position row*16 + col with row in
-// {2(t%4), 2(t%4)+1, 2(t%4)+8, 2(t%4)+9}[s%4] and col = t/4 + 8*(s/4).
-__device__ __forceinline__ int tc_perm(int i) {
-  const int t = i >> 3, s = i & 7;
-  const int r0 = (t & 3) * 2;
-  const int row = r0 + (s & 1) + ((s >> 1) & 1) * 8;
-  const int col = (t >> 2) + (s >> 2) * 8;
-  return row * 16 + col;
-}
-
-// Inverse of tc_perm: original position p -> encoded element.
-__device__ __forceinline__ int tc_perm_inv(int p) {
-  const int row = p >> 4, col = p & 15;
-  const int t = ((col & 7) << 2) | ((row & 7) >> 1);
-  const int s = (row & 1) | ((row >> 3) << 1) | ((col >> 3) << 2);
-  return (t << 3) | s;
-}
+using exl3::tc_perm;
+using exl3::tc_perm_inv;
 
 // ------------------------------------------------------- shared helpers
 

@@ -21,12 +21,18 @@
 //       hold an 8x8 sub-block of the lower triangle in registers; column k
 //       is published through a double-buffered LDS vector, one barrier per
 //       column.
+//   ldlq_gather_kernel / ldlq_scatter_kernel
+//       one LDLQ step's tile formation and write-back for every 16-row block
+//       of an encoder call, one 256-thread workgroup per tile: thread p moves
+//       tensor-core element p between the tile and row r, column 16 t + c of
+//       the block (W + compensation in; Wq, E = W - Wq and the states out).
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
 
 #include "../../include/exl3_layer.h"
 #include "exl3_errors.h"
+#include "exl3_layout.h"
 
 using exl3::check_launch;
 using exl3::set_error;
@@ -220,6 +226,45 @@ __global__ void __launch_bounds__(CH_THREADS)
   }
 }
 
+// ------------------------------------------------------------ LDLQ steps
+
+// Index of the block holding batch tile `tile` (blocks sorted by tile0).
+__device__ __forceinline__ int ldlq_block_of(const exl3_ldlq_block* __restrict__ blocks,
+                                             int nblocks, int64_t tile) {
+  int b = 0;
+  while (b + 1 < nblocks && blocks[b + 1].tile0 <= tile) ++b;
+  return b;
+}
+
+__global__ void __launch_bounds__(256)
+    ldlq_gather_kernel(const exl3_ldlq_block* __restrict__ blocks, int nblocks,
+                       float* __restrict__ x) {
+  const int64_t tile = blockIdx.x;
+  const exl3_ldlq_block blk = blocks[ldlq_block_of(blocks, nblocks, tile)];
+  const int p = threadIdx.x;
+  const int e = exl3::tc_perm(p);
+  const int64_t off = (int64_t)(e >> 4) * blk.n + (tile - blk.tile0) * 16 + (e & 15);
+  const float* w = reinterpret_cast<const float*>(blk.w);
+  const float* comp = reinterpret_cast<const float*>(blk.comp);
+  x[tile * 256 + p] = w[off] + comp[off];
+}
+
+__global__ void __launch_bounds__(256)
+    ldlq_scatter_kernel(const exl3_ldlq_block* __restrict__ blocks, int nblocks,
+                        const float* __restrict__ recon, const int16_t* __restrict__ idx) {
+  const int64_t tile = blockIdx.x;
+  const exl3_ldlq_block blk = blocks[ldlq_block_of(blocks, nblocks, tile)];
+  const int p = threadIdx.x;
+  const int e = exl3::tc_perm(p);
+  const int64_t t = tile - blk.tile0;
+  const int64_t off = (int64_t)(e >> 4) * blk.n + t * 16 + (e & 15);
+  const float v = recon[tile * 256 + p];
+  const float w = reinterpret_cast<const float*>(blk.w)[off];
+  reinterpret_cast<float*>(blk.wq)[off] = v;
+  reinterpret_cast<float*>(blk.err)[off] = w - v;
+  reinterpret_cast<int16_t*>(blk.states)[t * 256 + p] = idx[tile * 256 + p];
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------- C-ABI
@@ -284,5 +329,27 @@ int exl3_cholesky_diag_block(float* a, int64_t lda, int nb, int64_t offset, int3
 }
 
 int exl3_cholesky_block_order(void) { return CH_NB; }
+
+int exl3_ldlq_gather(const exl3_ldlq_block* blocks, int nblocks, int64_t tiles, float* x,
+                     void* stream) {
+  if (!blocks || !x) return set_error("ldlq_gather: NULL buffer");
+  if (nblocks < 1) return set_error("ldlq_gather: no blocks");
+  if (tiles < 1 || tiles > INT32_MAX) return set_error("ldlq_gather: bad tile count %lld",
+                                                       (long long)tiles);
+  hipLaunchKernelGGL(ldlq_gather_kernel, dim3((unsigned)tiles), dim3(256), 0, as_stream(stream),
+                     blocks, nblocks, x);
+  return check_launch("ldlq_gather");
+}
+
+int exl3_ldlq_scatter(const exl3_ldlq_block* blocks, int nblocks, int64_t tiles,
+                      const float* recon, const int16_t* idx, void* stream) {
+  if (!blocks || !recon || !idx) return set_error("ldlq_scatter: NULL buffer");
+  if (nblocks < 1) return set_error("ldlq_scatter: no blocks");
+  if (tiles < 1 || tiles > INT32_MAX) return set_error("ldlq_scatter: bad tile count %lld",
+                                                       (long long)tiles);
+  hipLaunchKernelGGL(ldlq_scatter_kernel, dim3((unsigned)tiles), dim3(256), 0, as_stream(stream),
+                     blocks, nblocks, recon, idx);
+  return check_launch("ldlq_scatter");
+}
 
 }  // extern "C"

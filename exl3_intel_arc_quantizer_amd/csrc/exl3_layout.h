@@ -178,4 +178,23 @@ constexpr int HDR_END_STATE = 1;  // int32 index
 constexpr int HDR_PRE_STATE = 2;  // int32 index
 constexpr int HDR_W_BYTES = 16;   // byte offset of the L fp16 inputs (cost-row mode)
 
+// tensor_core_perm (reference trellis_format.py:88-108): encoded element
+// 8t + s is original position row*16 + col with row in
+// {2(t%4), 2(t%4)+1, 2(t%4)+8, 2(t%4)+9}[s%4] and col = t/4 + 8*(s/4).
+EXL3_HD inline int tc_perm(int i) {
+  const int t = i >> 3, s = i & 7;
+  const int r0 = (t & 3) * 2;
+  const int row = r0 + (s & 1) + ((s >> 1) & 1) * 8;
+  const int col = (t >> 2) + (s >> 2) * 8;
+  return row * 16 + col;
+}
+
+// Inverse of tc_perm: original position p -> encoded element.
+EXL3_HD inline int tc_perm_inv(int p) {
+  const int row = p >> 4, col = p & 15;
+  const int t = ((col & 7) << 2) | ((row & 7) >> 1);
+  const int s = (row & 1) | ((row >> 3) << 1) | ((col >> 3) << 2);
+  return (t << 3) | s;
+}
+
 }  // namespace exl3

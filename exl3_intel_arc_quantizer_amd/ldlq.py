@@ -20,7 +20,7 @@ in tensor-core order. After a span its residual is propagated into
 A traversal is a chain of n / 16-tile encoder calls (256 tiles for a 4096
 wide projection: one workgroup per CU, half the encoder's occupancy).
 ``ldlq_lockstep`` walks independent projections side by side and encodes
-their blocks in one call per step.
+several of their blocks per call (``lockstep_schedule`` balances the calls).
 """
 
 from __future__ import annotations
@@ -40,8 +40,8 @@ DEFAULT_MAX_RETRIES = 10
 DEFAULT_BUF_SIZE_K = 128
 
 __all__ = ["DEFAULT_BLOCK_SIZE", "DEFAULT_SIGMA_REG", "DEFAULT_MAX_RETRIES", "DEFAULT_BUF_SIZE_K",
-           "BlockLDLResult", "cholesky_ex", "block_ldl", "LDLQResult", "ldlq", "ldlq_lockstep", "TileEncoder",
-           "make_xpu_tile_encoder", "make_gpu_tile_encoder"]
+           "BlockLDLResult", "cholesky_ex", "block_ldl", "LDLQResult", "ldlq", "ldlq_lockstep",
+           "lockstep_schedule", "TileEncoder", "make_xpu_tile_encoder", "make_gpu_tile_encoder"]
 
 
 @dataclass(frozen=True)
@@ -161,9 +161,18 @@ def _as_int16_states(indices: torch.Tensor) -> torch.Tensor:
 
 
 class _Traversal:
-    """One weight's bottom-up LDLQ walk, block by block: ``tiles(b)`` forms
-    block b's encoder input, ``store(b, ...)`` takes its result and, after a
-    span's last block, feeds the span residual into ``prod_cache``."""
+    """One weight's bottom-up LDLQ walk, block by block.
+
+    On a GPU the walk keeps E = W - Wq beside Wq: ``compensate(b)`` adds the
+    feedback of the rows already quantised below block b in its span to the
+    block's compensation rows (one GEMM), the HIP kernels
+    ``exl3_ldlq_gather`` / ``exl3_ldlq_scatter`` form the encoder's tiles
+    and write Wq, E and the states back for every block of a call at once,
+    and ``span_feedback(b)`` propagates a finished span's residual into the
+    compensation of the rows above it (one GEMM over those rows only: the
+    factor is lower triangular and rows at or below the span are never read
+    again). CPU tensors take the same steps as torch operations
+    (``tiles`` / ``store``)."""
 
     def __init__(self, weight: torch.Tensor, L: torch.Tensor, buf_size_k: int):
         if weight.dim() != 2 or weight.dtype != torch.float32:
@@ -187,12 +196,15 @@ class _Traversal:
             raise ValueError(f"rows ({k}) and columns ({n}) must be divisible by buf_size_k "
                              f"({buf_size_k})")
         device = weight.device
-        self.weight, self.L, self.buf_size_k = weight, L, buf_size_k
+        self.on_gpu = device.type == "cuda"
+        self.weight = weight.contiguous() if self.on_gpu else weight
+        self.L, self.buf_size_k = L, buf_size_k
         self.tiles_k, self.tiles_n, self.n = k // 16, n // 16, n
         self.perm = torch.as_tensor(tensor_core_perm(), dtype=torch.long, device=device)
         self.inv_perm = torch.as_tensor(tensor_core_perm_inv(), dtype=torch.long, device=device)
         self.prod_cache = torch.zeros((k, n), dtype=torch.float32, device=device)
         self.weight_q = torch.zeros((k, n), dtype=torch.float32, device=device)
+        self.err = torch.zeros((k, n), dtype=torch.float32, device=device) if self.on_gpu else None
         self.encoded = torch.zeros((k // 16, n // 16, 256), dtype=torch.int16, device=device)
         # (span start i, span end j, first row r0) in traversal order: spans
         # from the last, 16-row blocks inside a span from the last.
@@ -200,6 +212,31 @@ class _Traversal:
                        for j in range(k, 0, -buf_size_k) for bj in range(buf_size_k, 0, -16)]
         self.encoder_seconds = 0.0
         self.encoder_calls = 0
+
+    # ------------------------------------------------------- GPU steps
+
+    def compensate(self, b: int) -> None:
+        i, j, r0 = self.blocks[b]
+        r1 = r0 + 16
+        if r1 < j:
+            self.prod_cache[r0:r1].addmm_(self.L[r1:j, r0:r1].T, self.err[r1:j],
+                                          alpha=1.0, beta=1.0)
+
+    def span_feedback(self, b: int) -> None:
+        i, j, r0 = self.blocks[b]
+        if r0 == i and i > 0:
+            self.prod_cache[:i].addmm_(self.L[i:j, :i].T, self.err[i:j], alpha=1.0, beta=1.0)
+
+    def block_row(self, b: int, tile0: int) -> list:
+        """The ``exl3_ldlq_block`` fields of block b at batch tile ``tile0``."""
+        _, _, r0 = self.blocks[b]
+        row = r0 * self.n * 4
+        return [self.weight.data_ptr() + row, self.prod_cache.data_ptr() + row,
+                self.weight_q.data_ptr() + row, self.err.data_ptr() + row,
+                self.encoded.data_ptr() + (r0 // 16) * self.tiles_n * 256 * 2,
+                self.n, tile0, 0]
+
+    # ------------------------------------------------------- CPU steps
 
     def tiles(self, b: int) -> torch.Tensor:
         i, j, r0 = self.blocks[b]
@@ -216,17 +253,14 @@ class _Traversal:
     def store(self, b: int, quant_w: torch.Tensor, quant_i: torch.Tensor) -> None:
         i, j, r0 = self.blocks[b]
         device = self.weight.device
-        if tuple(quant_w.shape) != (self.tiles_n, 256) or tuple(quant_i.shape) != (self.tiles_n, 256):
-            raise ValueError("encode_tiles must return two (tiles_n, 256) tensors, got "
-                             f"{tuple(quant_w.shape)} / {tuple(quant_i.shape)}")
         quant_w = quant_w.to(device=device, dtype=torch.float32)[:, self.inv_perm]
         self.weight_q[r0:r0 + 16] = (quant_w.reshape(self.tiles_n, 16, 16).permute(1, 0, 2)
                                      .reshape(16, self.n))
         self.encoded[r0 // 16] = _as_int16_states(quant_i.to(device=device))
-        if r0 == i:
+        if r0 == i and i > 0:
             # Span residual into the feedback of the spans above.
-            self.prod_cache.addmm_(self.L[i:j].T, self.weight[i:j] - self.weight_q[i:j],
-                                   alpha=1.0, beta=1.0)
+            self.prod_cache[:i].addmm_(self.L[i:j, :i].T, self.weight[i:j] - self.weight_q[i:j],
+                                       alpha=1.0, beta=1.0)
 
     def result(self) -> "LDLQResult":
         return LDLQResult(weight_q=self.weight_q, encoded=self.encoded, tiles_k=self.tiles_k,
@@ -235,15 +269,95 @@ class _Traversal:
                           encoder_calls=self.encoder_calls)
 
 
+# Tiles one pass of the encoder runs at once on MI355X (256 CUs x two
+# 1024-thread workgroups): the unit a lockstep call's size is rounded to.
+LOCKSTEP_ROUND_TILES = 512
+
+
+def lockstep_schedule(block_counts: Sequence[int], tiles_per_block: Sequence[int],
+                      round_tiles: int = LOCKSTEP_ROUND_TILES) -> List[List[int]]:
+    """The walks that advance one block in each encoder call of a lockstep
+    traversal. There are max(block_counts) calls: the longest walk advances
+    in every one. A call first takes every walk that must advance (as many
+    blocks left as calls left), then the others, fewest spare calls first,
+    while the call stays within the mean tiles per call rounded up to a
+    multiple of ``round_tiles``. Walks keep their order inside a call. Every
+    walk's blocks stay in order, so each result equals its own traversal."""
+    if len(block_counts) != len(tiles_per_block):
+        raise ValueError("block_counts and tiles_per_block differ in length")
+    if not block_counts:
+        return []
+    calls = max(block_counts)
+    total = sum(b * t for b, t in zip(block_counts, tiles_per_block))
+    per_call = -(-total // calls)
+    target = max(round_tiles, -(-per_call // round_tiles) * round_tiles)
+    remaining = list(block_counts)
+    schedule = []
+    for c in range(calls):
+        left = calls - c
+        order = sorted((w for w in range(len(remaining)) if remaining[w] > 0),
+                       key=lambda w: (left - remaining[w], w))
+        load, members = 0, []
+        for w in order:
+            if remaining[w] == left or load + tiles_per_block[w] <= target:
+                members.append(w)
+                load += tiles_per_block[w]
+        members.sort()
+        for w in members:
+            remaining[w] -= 1
+        schedule.append(members)
+    return schedule
+
+
+def _block_table(walks: List[_Traversal], steps: List[List[Tuple[int, int]]]):
+    """Device table of ``exl3_ldlq_block`` rows for every call, and each
+    call's (first row, row count, tiles)."""
+    import numpy as np
+    for w in walks:
+        for t in (w.weight, w.prod_cache, w.weight_q, w.err, w.encoded):
+            if not t.is_contiguous():
+                raise ValueError("LDLQ buffers must be contiguous")
+    rows, spans = [], []
+    for call in steps:
+        tile0 = 0
+        first = len(rows)
+        for w, b in call:
+            rows.append(walks[w].block_row(b, tile0))
+            tile0 += walks[w].tiles_n
+        spans.append((first, len(call), tile0))
+    table = torch.from_numpy(np.asarray(rows, dtype=np.int64)).to(walks[0].weight.device)
+    return table, spans
+
+
 def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
                   synchronize: Optional[Callable[[], None]]) -> None:
-    """Step every walk's block b through one encoder call per b."""
-    use_events = synchronize is None and walks[0].weight.device.type == "cuda"
+    """Every walk's blocks through the encoder, several walks per call as
+    :func:`lockstep_schedule` assigns them."""
+    schedule = lockstep_schedule([len(w.blocks) for w in walks], [w.tiles_n for w in walks])
+    nxt = [0] * len(walks)
+    steps = []
+    for members in schedule:
+        steps.append([(w, nxt[w]) for w in members])
+        for w in members:
+            nxt[w] += 1
+    device = walks[0].weight.device
+    fused = walks[0].on_gpu
+    if fused:
+        from ._native import ldlq_gather, ldlq_scatter
+        table, spans = _block_table(walks, steps)
+    use_events = synchronize is None and fused
     pending = []      # (event pair, [(walk, tiles)]) read after the loop
-    for b in range(max(len(w.blocks) for w in walks)):
-        active = [w for w in walks if b < len(w.blocks)]
-        parts = [w.tiles(b) for w in active]
-        batch = parts[0] if len(parts) == 1 else torch.cat(parts)
+    for c, call in enumerate(steps):
+        if fused:
+            first, count, n_tiles = spans[c]
+            rows = table[first:first + count]
+            for w, b in call:
+                walks[w].compensate(b)
+            batch = torch.empty((n_tiles, 256), dtype=torch.float32, device=device)
+            ldlq_gather(rows, batch)
+        else:
+            parts = [walks[w].tiles(b) for w, b in call]
+            batch = parts[0] if len(parts) == 1 else torch.cat(parts)
         if use_events:
             ev0 = torch.cuda.Event(enable_timing=True)
             ev0.record()
@@ -254,21 +368,30 @@ def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
         if use_events:
             ev1 = torch.cuda.Event(enable_timing=True)
             ev1.record()
-            pending.append(((ev0, ev1), [(w, w.tiles_n) for w in active]))
+            pending.append(((ev0, ev1), [(walks[w], walks[w].tiles_n) for w, _ in call]))
         else:
             if synchronize is not None:
                 synchronize()
             dt = time.perf_counter() - t0
-            for w in active:
-                w.encoder_seconds += dt * w.tiles_n / batch.shape[0]
+            for w, _ in call:
+                walks[w].encoder_seconds += dt * walks[w].tiles_n / batch.shape[0]
         if tuple(quant_w.shape) != (batch.shape[0], 256) or tuple(quant_i.shape) != (batch.shape[0], 256):
             raise ValueError("encode_tiles must return two (tiles_n, 256) tensors, got "
                              f"{tuple(quant_w.shape)} / {tuple(quant_i.shape)}")
-        off = 0
-        for w in active:
-            w.store(b, quant_w[off:off + w.tiles_n], quant_i[off:off + w.tiles_n])
-            w.encoder_calls += 1
-            off += w.tiles_n
+        if fused:
+            recon = quant_w.to(device=device, dtype=torch.float32).contiguous()
+            idx = _as_int16_states(quant_i.to(device=device)).contiguous()
+            ldlq_scatter(rows, recon, idx)
+            for w, b in call:
+                walks[w].span_feedback(b)
+        else:
+            off = 0
+            for w, b in call:
+                walk = walks[w]
+                walk.store(b, quant_w[off:off + walk.tiles_n], quant_i[off:off + walk.tiles_n])
+                off += walk.tiles_n
+        for w, _ in call:
+            walks[w].encoder_calls += 1
     if pending:
         pending[-1][0][1].synchronize()
         for (ev0, ev1), members in pending:
@@ -310,11 +433,13 @@ def ldlq_lockstep(problems: Sequence[Tuple[torch.Tensor, torch.Tensor]],
                   encode_tiles: TileEncoder, buf_size_k: int = DEFAULT_BUF_SIZE_K,
                   synchronize: Callable[[], None] = None) -> List[LDLQResult]:
     """:func:`ldlq` on several independent (weight, L) problems at once:
-    block b of every problem that has one goes through the same encoder
-    call, so a launch carries the sum of their tile rows instead of one
-    projection's. Each result equals its own :func:`ldlq` run (tiles are
-    encoded independently of their batch); ``encoder_seconds`` splits each
-    call's time by the problems' tile counts."""
+    each encoder call carries the next block of several problems, as
+    :func:`lockstep_schedule` balances them (as many calls as the longest
+    problem has blocks, each near the mean size), so a launch holds ~1000
+    tiles instead of one projection's 64-768. Each result equals its own
+    :func:`ldlq` run (tiles are encoded independently of their batch);
+    ``encoder_seconds`` splits each call's time by the problems' tile
+    counts."""
     if not problems:
         return []
     walks = [_Traversal(w, L, buf_size_k) for w, L in problems]

@@ -45,6 +45,39 @@ int exl3_cholesky_diag_block(float* a, int64_t lda, int nb, int64_t offset, int3
 /* Largest block order exl3_cholesky_diag_block accepts (128). */
 int exl3_cholesky_block_order(void);
 
+/* One 16-row block of an LDLQ traversal inside an encoder call: device
+ * addresses (as integers) of the block's first row in W, in its
+ * compensation rows, in Wq and in E = W - Wq (all float, row stride n), of
+ * its (n / 16, 256) int16 states, and the block's first tile in the call's
+ * batch. A call's blocks are listed in batch order, back to back
+ * (tile0 of block b + 1 = tile0 + n / 16 of block b). The table itself is
+ * read by the kernels, so it lives in device memory. */
+typedef struct exl3_ldlq_block {
+  int64_t w;
+  int64_t comp;
+  int64_t wq;
+  int64_t err;
+  int64_t states;
+  int64_t n;
+  int64_t tile0;
+  int64_t reserved;
+} exl3_ldlq_block;
+
+/* Replaces the tile formation of one LDLQ step (ldlq.py:276-287) for every
+ * block of an encoder call: x[tile0 + t][p] = W[r][16 t + c] + comp[r][16 t + c]
+ * with (r, c) the row and column of tensor_core_perm(p) in a 16 x 16 tile.
+ * x is f32 [tiles][256]; tiles = the sum of the blocks' n / 16. */
+int exl3_ldlq_gather(const exl3_ldlq_block* blocks, int nblocks, int64_t tiles, float* x,
+                     void* stream);
+
+/* Replaces the write-back of one LDLQ step (ldlq.py:289-300) for every
+ * block of an encoder call, from the encoder's tensor-core-order outputs
+ * recon (f32 [tiles][256]) and idx (int16 [tiles][256]): Wq[r][16 t + c] =
+ * recon, E[r][16 t + c] = W - recon at the same position, and the block's
+ * states[t][p] = idx[tile0 + t][p]. */
+int exl3_ldlq_scatter(const exl3_ldlq_block* blocks, int nblocks, int64_t tiles,
+                      const float* recon, const int16_t* idx, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -158,3 +158,45 @@ def test_block_ldl_damping_retries_on_gpu(torch_mod):
     for b in range(16):
         np.testing.assert_array_equal(T[16 * b:16 * b + 16, 16 * b:16 * b + 16], np.eye(16))
     np.testing.assert_allclose(T, ref_T, rtol=0, atol=5e-4 * np.abs(ref_T).max())
+
+
+@pytest.mark.parametrize("shapes", [[(256, 128)], [(256, 128), (128, 256), (384, 384)]])
+def test_fused_ldlq_steps_match_host_traversal(torch_mod, shapes):
+    """exl3_ldlq_gather / exl3_ldlq_scatter (the GPU traversal) against the
+    torch traversal on the CPU, one problem and three in lockstep
+    (ldlq.py:163-309). The stand-in encoder halves its tiles (a continuous
+    map, so GEMM rounding differences stay at fp32 level) and returns states
+    that encode each element's batch position and call number, so every
+    state must land in the same place exactly."""
+    torch = torch_mod
+    from exl3_intel_arc_quantizer_amd.ldlq import ldlq_lockstep
+    probs = []
+    for s, (k, n) in enumerate(shapes):
+        rng = np.random.default_rng(100 + s)
+        W = rng.standard_normal((k, n)).astype(np.float32)
+        X = rng.standard_normal((4 * k, k)).astype(np.float32)
+        H = (X.T @ X) / np.float32(X.shape[0]) + np.float32(0.05) * np.eye(k, dtype=np.float32)
+        L, _, _ = ldlq_ref.block_ldl(H)
+        probs.append((W, L))
+    seen = {"cpu": [], "gpu": []}
+
+    def recorder(key):
+        def enc(tiles):
+            call = len(seen[key])
+            seen[key].append(tiles.cpu().clone())
+            pos = torch.arange(tiles.numel(), device=tiles.device).view(tiles.shape)
+            return tiles * 0.5, ((pos * 7 + call) & 0x7FFF).to(torch.int16)
+        return enc
+
+    cpu = ldlq_lockstep([(torch.from_numpy(W), torch.from_numpy(L)) for W, L in probs],
+                        recorder("cpu"), buf_size_k=64)
+    gpu = ldlq_lockstep([(torch.from_numpy(W).cuda(), torch.from_numpy(L).cuda())
+                         for W, L in probs], recorder("gpu"), buf_size_k=64)
+    assert len(seen["cpu"]) == len(seen["gpu"]) == max(k for k, _ in shapes) // 16
+    for a, b in zip(seen["cpu"], seen["gpu"]):
+        np.testing.assert_allclose(b.numpy(), a.numpy(), rtol=0, atol=1e-4)
+    for c, g in zip(cpu, gpu):
+        np.testing.assert_allclose(g.weight_q.cpu().numpy(), c.weight_q.numpy(), rtol=0,
+                                   atol=1e-4)
+        assert torch.equal(g.encoded.cpu(), c.encoded)
+        assert g.encoder_calls == c.encoder_calls

@@ -73,3 +73,40 @@ def test_ldlq_rejects_bad_shapes_and_encoder_output():
     with pytest.raises(ValueError, match="encode_tiles must return"):
         ldlq(Wt, Lt, lambda t: (t[:-1], t[:-1]))
     assert ldlq_lockstep([], _grid_torch) == []
+
+
+def test_lockstep_schedule_balances_calls():
+    """lockstep_schedule: as many calls as the longest walk has blocks, every
+    walk advancing exactly once per block, in order; a 9B-class layer's
+    projections (q, k, v, o, gate, up: 256 blocks; down: 768) spread over
+    768 calls of at most 1024 tiles instead of 256 calls of 2432 and 512
+    of 256."""
+    from exl3_intel_arc_quantizer_amd.ldlq import LOCKSTEP_ROUND_TILES, lockstep_schedule
+    blocks = [256, 256, 256, 256, 256, 256, 768]
+    tiles = [256, 64, 64, 256, 768, 768, 256]
+    sched = lockstep_schedule(blocks, tiles)
+    assert len(sched) == 768
+    assert [sum(w in call for call in sched) for w in range(7)] == blocks
+    loads = [sum(tiles[w] for w in call) for call in sched]
+    assert max(loads) == 1024 and min(loads) == 896
+    assert all(call == sorted(set(call)) for call in sched)
+    rng = np.random.default_rng(7)
+    for _ in range(50):
+        nw = int(rng.integers(1, 9))
+        b = [int(x) for x in rng.integers(1, 40, nw)]
+        t = [int(x) for x in rng.integers(1, 900, nw)]
+        sched = lockstep_schedule(b, t)
+        assert len(sched) == max(b)
+        assert [sum(w in call for call in sched) for w in range(nw)] == b
+        target = max(LOCKSTEP_ROUND_TILES,
+                     -(-(-(-sum(x * y for x, y in zip(b, t)) // max(b))) // LOCKSTEP_ROUND_TILES)
+                     * LOCKSTEP_ROUND_TILES)
+        left = list(b)
+        for c, call in enumerate(sched):
+            forced = [w for w in range(nw) if left[w] == len(sched) - c]
+            assert set(forced) <= set(call)
+            load = sum(t[w] for w in call)
+            assert load <= max(target, sum(t[w] for w in forced) + max(t)), (b, t, c)
+            for w in call:
+                left[w] -= 1
+    assert lockstep_schedule([], []) == []
