@@ -46,7 +46,9 @@ _SIGNATURES = {
     "exl3_probe_hfma": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
     # include/exl3_layer.h
     "exl3_hadamard128": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_vp]),
-    "exl3_block_rms": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
+    "exl3_block_rms": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_i64,
+                                _c_vp]),
+    "exl3_block_rms_workspace": (_c_i64, [_c_i64, _c_i64, _c_int, _c_int]),
     "exl3_cholesky_diag_block": (_c_int, [_c_vp, _c_i64, _c_int, _c_i64, _c_vp, _c_vp]),
     "exl3_cholesky_block_order": (_c_int, []),
     "exl3_ldlq_gather": (_c_int, [_c_vp, _c_int, _c_i64, _c_vp, _c_vp]),
@@ -478,9 +480,15 @@ def block_rms(x, out, dim: int, blocksize: int = 32) -> None:
             or out.device != x.device or out.numel() != n_out):
         raise RuntimeError(f"out must be a contiguous float32 tensor of {n_out} elements on "
                            f"{x.device}")
+    lib = load_library()
+    need = int(lib.exl3_block_rms_workspace(rows, cols, int(dim), int(blocksize)))
+    if need < 0:
+        raise RuntimeError(f"block_rms: invalid dim {dim} or blocksize {blocksize}")
     with torch.cuda.device(dev):
-        _check(load_library().exl3_block_rms(x.data_ptr(), out.data_ptr(), rows, cols, int(dim),
-                                             int(blocksize), _stream(dev)), "block_rms")
+        ws = torch.empty(max(need, 1), dtype=torch.float32, device=x.device)
+        _check(lib.exl3_block_rms(x.data_ptr(), out.data_ptr(), rows, cols, int(dim),
+                                  int(blocksize), ws.data_ptr(), ws.numel(), _stream(dev)),
+               "block_rms")
 
 
 def cholesky_block_order() -> int:

@@ -10,10 +10,10 @@
 //       levels 2..7 across lanes. Left (H @ x per 128-row block): one thread
 //       per column of a row block, the 128 values in registers; loads and
 //       stores are coalesced across the wave's 64 columns.
-//   block_rms_kernel
-//       sqrt(sum of squares / n) along one dimension, summed in slices of
-//       `blocksize` and the slice sums accumulated in slice order, one thread
-//       per output.
+//   block_rms_slices_kernel / block_rms_reduce_kernel
+//       sqrt(sum of squares / n) along one dimension: one thread per slice
+//       of `blocksize` sums its squares in order, then one thread per output
+//       accumulates the slice sums in slice order.
 //   cholesky_diag_kernel
 //       the unblocked Cholesky factorisation of one diagonal block (order
 //       <= 128) inside a blocked factorisation whose panel updates and
@@ -100,23 +100,39 @@ __global__ void __launch_bounds__(256)
 
 // --------------------------------------------------------------- block RMS
 
-// Output o reduces x[o * so + t * st] over t < n.
+// Output o reduces x[o * so + t * st] over t < n, in ns slices of bs.
+// Pass 1: one thread per (output, slice) sums the slice's squares in order
+// into ws: slice-major (ws[s * outputs + o]) when dim = 0, so that threads
+// of a wave read adjacent columns, output-major (ws[o * ns + s]) when
+// dim = 1, so that they read adjacent slices of one row.
 __global__ void __launch_bounds__(256)
-    block_rms_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t outputs,
-                     int64_t n, int64_t so, int64_t st, int blocksize) {
+    block_rms_slices_kernel(const float* __restrict__ x, float* __restrict__ ws, int64_t outputs,
+                            int64_t n, int64_t so, int64_t st, int bs, int64_t ns, int dim) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= outputs * ns) return;
+  const int64_t o = dim == 0 ? idx % outputs : idx / ns;
+  const int64_t s = dim == 0 ? idx / outputs : idx % ns;
+  const int64_t t0 = s * bs, t1 = t0 + bs < n ? t0 + bs : n;
+  const float* p = x + o * so;
+  float slice = 0.0f;
+  for (int64_t t = t0; t < t1; ++t) {
+    const float v = p[t * st];
+    const float sq = v * v;
+    slice = slice + sq;
+  }
+  ws[idx] = slice;
+}
+
+// Pass 2: one thread per output accumulates its slice sums in slice order.
+__global__ void __launch_bounds__(256)
+    block_rms_reduce_kernel(const float* __restrict__ ws, float* __restrict__ out,
+                            int64_t outputs, int64_t n, int64_t ns, int dim) {
   const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (o >= outputs) return;
-  const float* p = x + o * so;
   float acc = 0.0f;
-  for (int64_t s = 0; s < n; s += blocksize) {
-    const int64_t e = s + blocksize < n ? s + blocksize : n;
-    float slice = 0.0f;
-    for (int64_t t = s; t < e; ++t) {
-      const float v = p[t * st];
-      const float sq = v * v;
-      slice = slice + sq;
-    }
-    acc = (s == 0) ? slice : acc + slice;
+  for (int64_t s = 0; s < ns; ++s) {
+    const float v = dim == 0 ? ws[s * outputs + o] : ws[o * ns + s];
+    acc = (s == 0) ? v : acc + v;
   }
   out[o] = sqrtf(acc / (float)n);
 }
@@ -163,12 +179,15 @@ __global__ void __launch_bounds__(CH_THREADS)
   }
   __syncthreads();
 
+  // Only lower-triangle elements are ever published or stored, so the
+  // updates below run unmasked over whole sub-blocks: what they write above
+  // the diagonal (from stale column entries of rows < k) is never read.
   bool failed = false;
   for (int kb = 0; kb < CH_GRID; ++kb) {
 #pragma unroll
     for (int kc = 0; kc < CH_SB; ++kc) {
       const int k = kb * CH_SB + kc;
-      const float* ck = col[k & 1];
+      const float* ck = col[kc & 1];
       const float d = ck[k];
       if (t == 0 && !failed && !(d > 0.0f)) {
         failed = true;
@@ -176,52 +195,47 @@ __global__ void __launch_bounds__(CH_THREADS)
       }
       const float s = sqrtf(d);
       const float rs = 1.0f / s;
-      // Column k is final: its owners store it (L[k][k] = s, below it the
-      // published column times 1/s, the scaling of LAPACK's potf2).
-      if (active && bj == kb && k < nb) {
-#pragma unroll
-        for (int r = 0; r < CH_SB; ++r) {
-          const int i = i0 + r;
-          if (i >= k && i < nb) a[(int64_t)i * lda + k] = (i == k) ? s : ck[i] * rs;
-        }
-      }
-      // Rank-1 update of the trailing lower triangle.
-      if (active && j0 + CH_SB - 1 > k) {
+      if (active && bj >= kb) {
         float li[CH_SB], lj[CH_SB];
 #pragma unroll
         for (int r = 0; r < CH_SB; ++r) li[r] = ck[i0 + r] * rs;
 #pragma unroll
         for (int c = 0; c < CH_SB; ++c) lj[c] = ck[j0 + c] * rs;
+        if (bj == kb) {
+          // Column k is final (L[k][k] = s, below it the column times 1/s,
+          // the scaling of LAPACK's potf2); columns after it are updated.
 #pragma unroll
-        for (int r = 0; r < CH_SB; ++r) {
-#pragma unroll
-          for (int c = 0; c < CH_SB; ++c) {
-            const int i = i0 + r, j = j0 + c;
-            if (j > k && i >= j) v[r][c] = fmaf(-li[r], lj[c], v[r][c]);
-          }
-        }
-      }
-      // Publish column k + 1 (rows k + 1 and below) for the next step.
-      if (k + 1 < CH_NB) {
-        const int nkb = (kc == CH_SB - 1) ? kb + 1 : kb;
-        if (active && bj == nkb) {
+          for (int r = 0; r < CH_SB; ++r) v[r][kc] = li[r];
+          if (bi == kb) v[kc][kc] = s;
 #pragma unroll
           for (int r = 0; r < CH_SB; ++r) {
-            const int i = i0 + r;
-            if (i >= k + 1) col[(k + 1) & 1][i] = v[r][(kc + 1) % CH_SB];
+#pragma unroll
+            for (int c = kc + 1; c < CH_SB; ++c) v[r][c] = fmaf(-li[r], lj[c], v[r][c]);
           }
+        } else {
+#pragma unroll
+          for (int r = 0; r < CH_SB; ++r) {
+#pragma unroll
+            for (int c = 0; c < CH_SB; ++c) v[r][c] = fmaf(-li[r], lj[c], v[r][c]);
+          }
+        }
+        // Publish column k + 1 for the next step.
+        const int nkb = (kc == CH_SB - 1) ? kb + 1 : kb;
+        if (bj == nkb) {
+#pragma unroll
+          for (int r = 0; r < CH_SB; ++r) col[(kc + 1) & 1][i0 + r] = v[r][(kc + 1) % CH_SB];
         }
       }
       __syncthreads();
     }
   }
-  // Zeros above the diagonal.
+  // L on and below the diagonal, zeros above.
 #pragma unroll
   for (int r = 0; r < CH_SB; ++r) {
 #pragma unroll
     for (int c = 0; c < CH_SB; ++c) {
       const int i = i0 + r, j = j0 + c;
-      if (j > i && i < nb && j < nb) a[(int64_t)i * lda + j] = 0.0f;
+      if (i < nb && j < nb) a[(int64_t)i * lda + j] = (j <= i && active) ? v[r][c] : 0.0f;
     }
   }
 }
@@ -299,19 +313,35 @@ int exl3_hadamard128(const float* in, float* out, int64_t rows, int64_t cols, in
   return check_launch("hadamard128");
 }
 
+int64_t exl3_block_rms_workspace(int64_t rows, int64_t cols, int dim, int blocksize) {
+  if (rows <= 0 || cols <= 0 || (dim != 0 && dim != 1) || blocksize <= 0) return -1;
+  const int64_t outputs = dim == 0 ? cols : rows, n = dim == 0 ? rows : cols;
+  return outputs * ((n + blocksize - 1) / blocksize);
+}
+
 int exl3_block_rms(const float* x, float* out, int64_t rows, int64_t cols, int dim, int blocksize,
-                   void* stream) {
-  if (!x || !out) return set_error("block_rms: NULL buffer");
+                   float* workspace, int64_t workspace_elems, void* stream) {
+  if (!x || !out || !workspace) return set_error("block_rms: NULL buffer");
   if (rows <= 0 || cols <= 0) return set_error("block_rms: empty matrix");
   if (dim != 0 && dim != 1) return set_error("block_rms: dim must be 0 or 1, got %d", dim);
   if (blocksize <= 0) return set_error("block_rms: blocksize must be positive, got %d", blocksize);
+  const int64_t need = exl3_block_rms_workspace(rows, cols, dim, blocksize);
+  if (workspace_elems < need)
+    return set_error("block_rms: workspace holds %lld floats, %lld needed",
+                     (long long)workspace_elems, (long long)need);
   const int64_t outputs = dim == 0 ? cols : rows;
   const int64_t n = dim == 0 ? rows : cols;
   const int64_t so = dim == 0 ? 1 : cols, st = dim == 0 ? cols : 1;
-  unsigned blocks;
-  if (exl3::grid_1d(outputs, 256, &blocks, "block_rms")) return 1;
-  hipLaunchKernelGGL(block_rms_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), x, out,
-                     outputs, n, so, st, blocksize);
+  const int64_t ns = (n + blocksize - 1) / blocksize;
+  unsigned b1, b2;
+  if (exl3::grid_1d(outputs * ns, 256, &b1, "block_rms")) return 1;
+  if (exl3::grid_1d(outputs, 256, &b2, "block_rms")) return 1;
+  hipStream_t sm = as_stream(stream);
+  hipLaunchKernelGGL(block_rms_slices_kernel, dim3(b1), dim3(256), 0, sm, x, workspace, outputs, n,
+                     so, st, blocksize, ns, dim);
+  if (check_launch("block_rms")) return 1;
+  hipLaunchKernelGGL(block_rms_reduce_kernel, dim3(b2), dim3(256), 0, sm, workspace, out, outputs,
+                     n, ns, dim);
   return check_launch("block_rms");
 }
 

@@ -29,9 +29,15 @@ int exl3_hadamard128(const float* in, float* out, int64_t rows, int64_t cols, in
 /* Replaces block_rms (regularize.py:41-56): out = sqrt(S / n), S the sum of
  * squares along `dim` (0: over rows, one output per column; 1: over
  * columns, one per row) taken in slices of `blocksize` whose sums are
- * accumulated in slice order. */
+ * accumulated in slice order. workspace: device floats, at least
+ * exl3_block_rms_workspace(rows, cols, dim, blocksize) of them (the slice
+ * sums). */
 int exl3_block_rms(const float* x, float* out, int64_t rows, int64_t cols, int dim, int blocksize,
-                   void* stream);
+                   float* workspace, int64_t workspace_elems, void* stream);
+
+/* Floats of workspace exl3_block_rms needs (outputs x slices), or -1 for
+ * invalid arguments. */
+int64_t exl3_block_rms_workspace(int64_t rows, int64_t cols, int dim, int blocksize);
 
 /* The diagonal-block step of a blocked Cholesky factorisation, which
  * replaces torch.linalg.cholesky_ex in block_ldl (ldlq.py:76-142): factors
