@@ -329,28 +329,37 @@ def _block_table(walks: List[_Traversal], steps: List[List[Tuple[int, int]]]):
     return table, spans
 
 
-def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
-                  synchronize: Optional[Callable[[], None]]) -> None:
-    """Every walk's blocks through the encoder, several walks per call as
-    :func:`lockstep_schedule` assigns them."""
-    schedule = lockstep_schedule([len(w.blocks) for w in walks], [w.tiles_n for w in walks])
-    nxt = [0] * len(walks)
-    steps = []
-    for members in schedule:
-        steps.append([(w, nxt[w]) for w in members])
-        for w in members:
-            nxt[w] += 1
-    device = walks[0].weight.device
-    fused = walks[0].on_gpu
-    if fused:
+class _Lane:
+    """A set of walks whose blocks share encoder calls, as
+    :func:`lockstep_schedule` assigns them, with its own encoder adapter and
+    (on a GPU with several lanes) its own stream."""
+
+    def __init__(self, walks: List[_Traversal], encode_tiles: TileEncoder,
+                 synchronize: Optional[Callable[[], None]], stream=None):
+        self.walks, self.encode_tiles, self.synchronize = walks, encode_tiles, synchronize
+        self.stream = stream
+        schedule = lockstep_schedule([len(w.blocks) for w in walks], [w.tiles_n for w in walks])
+        nxt = [0] * len(walks)
+        self.steps = []
+        for members in schedule:
+            self.steps.append([(w, nxt[w]) for w in members])
+            for w in members:
+                nxt[w] += 1
+        self.device = walks[0].weight.device
+        self.fused = walks[0].on_gpu
+        if self.fused:
+            self.table, self.spans = _block_table(walks, self.steps)
+        self.use_events = synchronize is None and self.fused
+        self.pending = []      # (event pair, [(walk, tiles)]) read after the loop
+        self.done = 0
+
+    def issue(self) -> None:
+        """Queue the lane's next encoder call and the steps around it."""
         from ._native import ldlq_gather, ldlq_scatter
-        table, spans = _block_table(walks, steps)
-    use_events = synchronize is None and fused
-    pending = []      # (event pair, [(walk, tiles)]) read after the loop
-    for c, call in enumerate(steps):
-        if fused:
-            first, count, n_tiles = spans[c]
-            rows = table[first:first + count]
+        walks, call, device = self.walks, self.steps[self.done], self.device
+        if self.fused:
+            first, count, n_tiles = self.spans[self.done]
+            rows = self.table[first:first + count]
             for w, b in call:
                 walks[w].compensate(b)
             batch = torch.empty((n_tiles, 256), dtype=torch.float32, device=device)
@@ -358,27 +367,27 @@ def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
         else:
             parts = [walks[w].tiles(b) for w, b in call]
             batch = parts[0] if len(parts) == 1 else torch.cat(parts)
-        if use_events:
+        if self.use_events:
             ev0 = torch.cuda.Event(enable_timing=True)
             ev0.record()
-        elif synchronize is not None:
-            synchronize()
+        elif self.synchronize is not None:
+            self.synchronize()
         t0 = time.perf_counter()
-        quant_w, quant_i = encode_tiles(batch)
-        if use_events:
+        quant_w, quant_i = self.encode_tiles(batch)
+        if self.use_events:
             ev1 = torch.cuda.Event(enable_timing=True)
             ev1.record()
-            pending.append(((ev0, ev1), [(walks[w], walks[w].tiles_n) for w, _ in call]))
+            self.pending.append(((ev0, ev1), [(walks[w], walks[w].tiles_n) for w, _ in call]))
         else:
-            if synchronize is not None:
-                synchronize()
+            if self.synchronize is not None:
+                self.synchronize()
             dt = time.perf_counter() - t0
             for w, _ in call:
                 walks[w].encoder_seconds += dt * walks[w].tiles_n / batch.shape[0]
         if tuple(quant_w.shape) != (batch.shape[0], 256) or tuple(quant_i.shape) != (batch.shape[0], 256):
             raise ValueError("encode_tiles must return two (tiles_n, 256) tensors, got "
                              f"{tuple(quant_w.shape)} / {tuple(quant_i.shape)}")
-        if fused:
+        if self.fused:
             recon = quant_w.to(device=device, dtype=torch.float32).contiguous()
             idx = _as_int16_states(quant_i.to(device=device)).contiguous()
             ldlq_scatter(rows, recon, idx)
@@ -392,16 +401,113 @@ def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
                 off += walk.tiles_n
         for w, _ in call:
             walks[w].encoder_calls += 1
-    if pending:
-        pending[-1][0][1].synchronize()
-        for (ev0, ev1), members in pending:
-            dt = ev0.elapsed_time(ev1) / 1e3
-            total = sum(t for _, t in members)
-            for w, t in members:
-                w.encoder_seconds += dt * t / total
-    check_finite = getattr(encode_tiles, "check_finite", None)
-    if check_finite is not None:
-        check_finite()
+        self.done += 1
+
+    def intervals(self, ref) -> List[Tuple[float, float]]:
+        """Start and end of every encoder call, seconds after event ``ref``."""
+        return [(ref.elapsed_time(ev0) / 1e3, ref.elapsed_time(ev1) / 1e3)
+                for (ev0, ev1), _ in self.pending]
+
+    def finish(self, scale: float = 1.0) -> None:
+        """Credit each call's duration (times ``scale``) to its walks by
+        tile share, then raise on NaN inputs the encoder counted."""
+        if self.pending:
+            self.pending[-1][0][1].synchronize()
+            for (ev0, ev1), members in self.pending:
+                dt = ev0.elapsed_time(ev1) / 1e3 * scale
+                total = sum(t for _, t in members)
+                for w, t in members:
+                    w.encoder_seconds += dt * t / total
+        check_finite = getattr(self.encode_tiles, "check_finite", None)
+        if check_finite is not None:
+            check_finite()
+
+
+def _union_seconds(intervals: List[Tuple[float, float]]) -> float:
+    total, end = 0.0, None
+    for a, b in sorted(intervals):
+        if end is None or a > end:
+            total += b - a
+            end = b
+        elif b > end:
+            total += b - end
+            end = b
+    return total
+
+
+def _lanes_of(walks: List[_Traversal]) -> List[List[int]]:
+    """Walks split into two lanes: those with the most blocks (the
+    traversal's critical chain of calls) and the rest; one lane when every
+    walk has the same length. On a 9B-class layer (down_proj 768 blocks,
+    the other six 256) this measured 1.22 s against 1.30 s for one lane,
+    and against 1.24-1.30 s for splits that move the smaller projections
+    into the first lane."""
+    longest = max(len(w.blocks) for w in walks)
+    lanes = [[i for i, w in enumerate(walks) if len(w.blocks) == longest],
+             [i for i, w in enumerate(walks) if len(w.blocks) < longest]]
+    return [lane for lane in lanes if lane]
+
+
+def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
+                  synchronize: Optional[Callable[[], None]]) -> None:
+    """Every walk's blocks through the encoder, several walks per call as
+    :func:`lockstep_schedule` assigns them.
+
+    On a GPU, when the walks differ in length and the encoder can ``fork``
+    a second adapter, the walks run as two lanes (:func:`_lanes_of`) on two
+    streams, their calls queued alternately in proportion to their counts:
+    one lane's latency-bound tracebacks and small launches then overlap the
+    other's forward passes. Every walk's blocks still go through the
+    encoder in order, so each result is unchanged. A walk's
+    ``encoder_seconds`` is its tile share of each call's duration, the
+    durations scaled so that all calls together count the time during which
+    any was running."""
+    groups = _lanes_of(walks)
+    concurrent = (len(groups) > 1 and walks[0].on_gpu and synchronize is None
+                  and callable(getattr(encode_tiles, "fork", None)))
+    if not concurrent:
+        lane = _Lane(walks, encode_tiles, synchronize)
+        while lane.done < len(lane.steps):
+            lane.issue()
+        lane.finish()
+        return
+    device = walks[0].weight.device
+    origin = torch.cuda.current_stream(device)
+    encoders = [encode_tiles] + [encode_tiles.fork() for _ in groups[1:]]
+    # The first lane stays on the caller's stream: two pool streams can share
+    # one hardware queue, which would serialise the lanes again.
+    ref = torch.cuda.Event(enable_timing=True)
+    ref.record(origin)
+    lanes = []
+    for g, (members, enc) in enumerate(zip(groups, encoders)):
+        stream = origin if g == 0 else torch.cuda.Stream(device=device)
+        if g:
+            stream.wait_stream(origin)
+        with torch.cuda.stream(stream):
+            lanes.append(_Lane([walks[i] for i in members], enc, None, stream))
+    try:
+        while True:
+            open_lanes = [ln for ln in lanes if ln.done < len(ln.steps)]
+            if not open_lanes:
+                break
+            lane = min(open_lanes, key=lambda ln: (ln.done + 1) / len(ln.steps))
+            with torch.cuda.stream(lane.stream):
+                lane.issue()
+        for lane in lanes[1:]:
+            origin.wait_stream(lane.stream)
+        # Calls of different lanes overlap: their durations are scaled so
+        # that together they add up to the time any encoder call was running.
+        for lane in lanes:
+            if lane.pending:
+                lane.pending[-1][0][1].synchronize()
+        spans = [iv for lane in lanes for iv in lane.intervals(ref)]
+        busy = sum(b - a for a, b in spans)
+        scale = _union_seconds(spans) / busy if busy > 0 else 1.0
+        for lane in lanes:
+            lane.finish(scale)
+    finally:
+        for enc in encoders[1:]:
+            enc.encoder.arena.release()
 
 
 def ldlq(weight: torch.Tensor, L: torch.Tensor, encode_tiles: TileEncoder,

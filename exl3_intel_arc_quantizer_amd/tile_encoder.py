@@ -5,7 +5,8 @@ tensor-core order and returns ``(reconstructed, indices)``, both
 ``(tiles_n, 256)``: the reconstruction in tensor-core order (fp16 values as
 float32) and the indices as 16-bit states in int16. ``make_xpu_tile_encoder``
 keeps the reference's name and signature; the returned callable also
-carries ``.K`` and ``.cb`` as the reference's does.
+carries ``.K`` and ``.cb`` as the reference's does, and ``.fork()`` gives a
+second adapter with its own scratch for calls on another stream.
 
 Unlike the reference adapter, which converts every call's tiles to numpy and
 back (ldlq.py:370-380), this one keeps a CUDA input on the device: the
@@ -73,10 +74,22 @@ def make_xpu_tile_encoder(K: int = 2, device_index: int = 0, arena=None, sg_size
             check_finite()
         return recon, idx
 
+    def fork():
+        """Another adapter with the same settings, its own scratch arena (same
+        memory policy) and NaN counter: for calls queued on another stream
+        while this one's are in flight."""
+        from .gpu_quantizer import ScratchArena
+        return make_xpu_tile_encoder(
+            K=K, device_index=device_index,
+            arena=ScratchArena(policy=encoder.arena.policy, device_index=device_index),
+            sg_size=sg_size, force_global_costs=force_global_costs,
+            traceback_mode=traceback_mode, asynchronous=asynchronous, cb=cb)
+
     encode.K = K
     encode.cb = cb
     encode.encoder = encoder
     encode.check_finite = check_finite
+    encode.fork = fork
     return encode
 
 

@@ -182,3 +182,40 @@ def test_ldlq_async_encoder_timing_and_nan(torch_mod):
         enc.check_finite()
     finally:
         enc.encoder.arena.release()
+
+
+def test_decoder_layer_two_lanes_equal_sequential(torch_mod):
+    """Lockstep with the walks split into two lanes on two streams (down_proj,
+    twice as many blocks, and the rest) gives every projection the states
+    and reconstruction of the one-at-a-time order, and the encoder time it
+    reports stays within the traversal's wall time."""
+    from exl3_intel_arc_quantizer_amd import ldlq as ldlq_mod
+    from exl3_intel_arc_quantizer_amd.layer_quant import (hessian_from_activations,
+                                                          quantize_decoder_layer)
+    torch = torch_mod
+    nn = torch.nn
+    torch.manual_seed(1)
+    layer = nn.Module()
+    layer.self_attn = nn.Module()
+    layer.mlp = nn.Module()
+    layer.self_attn.q_proj = nn.Linear(256, 256, bias=False)
+    layer.self_attn.k_proj = nn.Linear(256, 128, bias=False)
+    layer.mlp.gate_proj = nn.Linear(256, 512, bias=False)
+    layer.mlp.down_proj = nn.Linear(512, 256, bias=False)
+    layer = layer.cuda()
+    rng = np.random.default_rng(31)
+    h256, _ = hessian_from_activations(
+        torch.from_numpy(rng.standard_normal((1024, 256)).astype(np.float32)).cuda())
+    h512, _ = hessian_from_activations(
+        torch.from_numpy(rng.standard_normal((1024, 512)).astype(np.float32)).cuda())
+    hess = {"self_attn.q_proj": h256, "self_attn.k_proj": h256, "mlp.gate_proj": h256,
+            "mlp.down_proj": h512}
+    walks = [type("W", (), {"blocks": [0] * b, "tiles_n": t})()
+             for b, t in ((16, 16), (16, 8), (16, 32), (32, 16))]
+    assert ldlq_mod._lanes_of(walks) == [[3], [0, 1, 2]]
+    rep = quantize_decoder_layer(layer, hess, K=2)
+    seq = quantize_decoder_layer(layer, hess, K=2, lockstep=False)
+    for name, r in rep.module_results.items():
+        assert torch.equal(r.encoded, seq.module_results[name].encoded), name
+        assert torch.equal(r.w_hat, seq.module_results[name].w_hat), name
+    assert 0 < rep.encoder_seconds <= rep.extra["traversal_seconds"] * 1.05

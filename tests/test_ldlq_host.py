@@ -110,3 +110,19 @@ def test_lockstep_schedule_balances_calls():
             for w in call:
                 left[w] -= 1
     assert lockstep_schedule([], []) == []
+
+
+def test_lanes_and_union_of_intervals():
+    """The two-lane split (longest walks, the rest) and the union length the
+    overlapping encoder calls are scaled to."""
+    from exl3_intel_arc_quantizer_amd.ldlq import _lanes_of, _union_seconds
+
+    def walk(b, t):
+        return type("W", (), {"blocks": [0] * b, "tiles_n": t})()
+
+    nine_b = [walk(256, 256), walk(256, 64), walk(256, 64), walk(256, 256), walk(256, 768),
+              walk(256, 768), walk(768, 256)]
+    assert _lanes_of(nine_b) == [[6], [0, 1, 2, 3, 4, 5]]
+    assert _lanes_of([walk(16, 8), walk(16, 32)]) == [[0, 1]]
+    assert _union_seconds([(0.0, 1.0), (0.5, 2.0), (3.0, 4.0), (3.5, 3.6)]) == pytest.approx(3.0)
+    assert _union_seconds([]) == 0.0
