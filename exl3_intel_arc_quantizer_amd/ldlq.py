@@ -474,18 +474,23 @@ def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
     device = walks[0].weight.device
     origin = torch.cuda.current_stream(device)
     encoders = [encode_tiles] + [encode_tiles.fork() for _ in groups[1:]]
+    # Tracebacks by per-row tree loads: the streamed kernel reads whole rows,
+    # bandwidth the other lane's forward passes need (9B-class layer: 1.20 s
+    # against 1.23-1.26 s). The choice is process-wide while the lanes run.
+    from ._native import set_traceback_policy
+    previous_policy = set_traceback_policy("rows")
     # The first lane stays on the caller's stream: two pool streams can share
     # one hardware queue, which would serialise the lanes again.
     ref = torch.cuda.Event(enable_timing=True)
     ref.record(origin)
     lanes = []
-    for g, (members, enc) in enumerate(zip(groups, encoders)):
-        stream = origin if g == 0 else torch.cuda.Stream(device=device)
-        if g:
-            stream.wait_stream(origin)
-        with torch.cuda.stream(stream):
-            lanes.append(_Lane([walks[i] for i in members], enc, None, stream))
     try:
+        for g, (members, enc) in enumerate(zip(groups, encoders)):
+            stream = origin if g == 0 else torch.cuda.Stream(device=device)
+            if g:
+                stream.wait_stream(origin)
+            with torch.cuda.stream(stream):
+                lanes.append(_Lane([walks[i] for i in members], enc, None, stream))
         while True:
             open_lanes = [ln for ln in lanes if ln.done < len(ln.steps)]
             if not open_lanes:
@@ -506,6 +511,9 @@ def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
         for lane in lanes:
             lane.finish(scale)
     finally:
+        for lane in lanes[1:]:
+            origin.wait_stream(lane.stream)
+        set_traceback_policy(previous_policy)
         for enc in encoders[1:]:
             enc.encoder.arena.release()
 
