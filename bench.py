@@ -20,7 +20,7 @@ HIP events on the stream the kernel runs on. Peak = 256 CU * 64 lanes * 2
 157.3 TFLOP/s fp16 vector rate counts each FMA twice).
 
 ``traffic``: HBM bytes per forward launch from the committed rocprofv3 PMC
-summary (profiles/forward_pass_pmc_config2.md): FETCH_SIZE x 2 + WRITE_SIZE
+summary (profiles/forward_pass_pmc_configs1.md): FETCH_SIZE x 2 + WRITE_SIZE
 x 1.0 per dispatch, the factors a 1 GiB device copy reads on the same
 counters; null when the summary has no row for the kernel.
 
@@ -103,7 +103,7 @@ def time_steps(batch, steps, warmup, torch):
 
 
 PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                           "forward_pass_pmc_config2.md")
+                           "forward_pass_pmc_configs1.md")
 
 
 def pmc_traffic(K, tiles):
@@ -153,7 +153,7 @@ def forward_kernel_roofline(batch, torch, reps=3):
             "ops_note": "fp16 element-ops: tiles*256 steps*65536 candidates*3 (sub, FMA, "
                         "compare-select); peak 256 CU*64 lanes*2 halves*2.4 GHz",
             "traffic_note": "HBM bytes per launch: rocprofv3 FETCH_SIZE*2 + WRITE_SIZE*1.0 "
-                            "(copy-kernel calibration), profiles/forward_pass_pmc_config2.md"}
+                            "(copy-kernel calibration), profiles/forward_pass_pmc_configs1.md"}
 
 
 def _numpy_encode_one(args):
