@@ -205,7 +205,7 @@ def _synthetic_activations(rng, tokens, width, outlier_frac=0.05):
     return X
 
 
-def run_layer_config(torch, K=4):
+def run_layer_config(torch, K=4, gss=False):
     """one 4096x4096 linear layer, W ~ N(0, 0.02^2) (seed 3),
     Hessian X^T X / 8192 from bf16 activations [8192, 4096] (seed 4, 5 % of
     channels x10), damped 1 %, Hadamard-rotated inside the driver, LDLQ with
@@ -219,14 +219,15 @@ def run_layer_config(torch, K=4):
     X = X.to(torch.bfloat16).cuda()
     H, damp = hessian_from_activations(X)
     del X
-    quantize_linear_module("warmup", W[:256, :256].cuda(), H[:256, :256].contiguous(), K=K)
+    quantize_linear_module("warmup", W[:256, :256].cuda(), H[:256, :256].contiguous(), K=K,
+                           skip_g_scale=not gss)
     torch.cuda.synchronize()
     # A 0.2 s run is sensitive to clock ramp and host jitter: time three
     # full-size runs and report the median one.
     runs = []
     for _ in range(3):
         t0 = time.perf_counter()
-        res = quantize_linear_module("layer", W.cuda(), H, K=K)
+        res = quantize_linear_module("layer", W.cuda(), H, K=K, skip_g_scale=not gss)
         torch.cuda.synchronize()
         runs.append((time.perf_counter() - t0, res))
     runs.sort(key=lambda r: r[0])
@@ -236,7 +237,8 @@ def run_layer_config(torch, K=4):
     return {"metric": "LDLQ-driven 4096x4096 layer, K=4, 1 MI355X: wall time", "value": round(wall, 3),
             "unit": "s", "higher_is_better": False, "n_gpus": 1, "dtype": "fp16", "data": "synthetic",
             "config": {"workload": "configs[3]", "K": K, "buf_size_k": 128, "tiles": tiles,
-                       "encoder_calls": m.encoder_calls},
+                       "encoder_calls": m.encoder_calls, "global_scale_search": gss},
+            "g_scale": m.g_scale,
             "tiles_per_s": round(tiles / wall, 1),
             "runs_seconds": [round(r[0], 3) for r in runs],
             "encoder_seconds": round(m.encoder_seconds, 3),
@@ -248,7 +250,7 @@ def run_layer_config(torch, K=4):
                                "(tests/test_gpu_layer.py); a full-size CPU run is hours"}
 
 
-def run_decoder_config(torch, K=4, cpu_tiles_per_s=None, lockstep=True):
+def run_decoder_config(torch, K=4, cpu_tiles_per_s=None, lockstep=True, gss=False):
     """configs[4]: a 9B-class decoder layer (hidden 4096; q, o 4096x4096;
     k, v 1024x4096; gate, up 12288x4096; down 4096x12288), random-init weights
     (torch seed 5), Hessians per shared-input group from synthetic bf16
@@ -286,17 +288,18 @@ def run_decoder_config(torch, K=4, cpu_tiles_per_s=None, lockstep=True):
     # A model conversion runs this once per layer; the first layer of a
     # process also pays rocSOLVER / hipBLASLt kernel loading, so the timed
     # run is the second conversion of the same shapes (the steady state).
-    first = quantize_decoder_layer(layer, hess, K=K, lockstep=lockstep)
+    first = quantize_decoder_layer(layer, hess, K=K, lockstep=lockstep, skip_g_scale=not gss)
     first_wall = first.total_elapsed_seconds
     del first
-    rep = quantize_decoder_layer(layer, hess, K=K, lockstep=lockstep)
+    rep = quantize_decoder_layer(layer, hess, K=K, lockstep=lockstep, skip_g_scale=not gss)
     wall = rep.total_elapsed_seconds
     calls = sum(r.metrics.encoder_calls for r in rep.module_results.values())
     out = {"metric": "9B-class decoder layer conversion, K=4, 1 MI355X: wall time",
            "value": round(wall, 3), "unit": "s", "higher_is_better": False, "n_gpus": 1,
            "dtype": "fp16", "data": "synthetic",
            "config": {"workload": "configs[4]", "K": K, "tiles": rep.tiles,
-                      "module_encoder_calls": calls, "lockstep": lockstep},
+                      "module_encoder_calls": calls, "lockstep": lockstep,
+                      "global_scale_search": gss},
            "tiles_per_s": round(rep.tiles / wall, 1),
            "encoder_seconds": round(rep.encoder_seconds, 3),
            "encoder_share": round(rep.encoder_seconds / wall, 4),
@@ -308,7 +311,8 @@ def run_decoder_config(torch, K=4, cpu_tiles_per_s=None, lockstep=True):
            "modules": {n: {"shape_kn": list(r.original_shape),
                            "seconds": round(r.metrics.elapsed_seconds, 3),
                            "encoder_seconds": round(r.metrics.encoder_seconds, 3),
-                           "normalized_proxy_loss": r.metrics.normalized_proxy_loss}
+                           "normalized_proxy_loss": r.metrics.normalized_proxy_loss,
+                           "g_scale": r.metrics.g_scale}
                        for n, r in rep.module_results.items()}}
     if cpu_tiles_per_s:
         out["cpu_encoder_extrapolated_seconds"] = round(rep.tiles / cpu_tiles_per_s, 1)
@@ -361,6 +365,8 @@ def main() -> int:
                     help="configs[4]: 9B-class decoder layer conversion (its own JSON line)")
     ap.add_argument("--host-api", action="store_true",
                     help="configs[1] through encode_batch_detailed (numpy in/out; PCIe-inclusive)")
+    ap.add_argument("--gss", action="store_true",
+                    help="with --layer / --decoder: run the global-scale search (skip_g_scale=False)")
     ap.add_argument("--sequential", action="store_true",
                     help="with --decoder: one projection at a time (the reference's order)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -385,9 +391,9 @@ def main() -> int:
         import torch
         if args.decoder and not args.no_cpu_baseline:
             cpu = cpu_baseline(tiles, 4)
-        line = (run_layer_config(torch) if args.layer else
+        line = (run_layer_config(torch, gss=args.gss) if args.layer else
                 run_decoder_config(torch, cpu_tiles_per_s=cpu["value"] if cpu else None,
-                                   lockstep=not args.sequential))
+                                   lockstep=not args.sequential, gss=args.gss))
         print(json.dumps(line), flush=True)
         return 0
     if not args.no_cpu_baseline and not args.profile_forward:

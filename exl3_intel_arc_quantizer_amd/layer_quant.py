@@ -238,6 +238,22 @@ def _prepare_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int, cb
                            prep_seconds=time.time() - t0)
 
 
+def _apply_global_scales(prepared: List[_PreparedModule], tile_encoder: TileEncoder) -> None:
+    """Global-scale search (gss.py:187-207) for several regularised
+    projections in one batch, applied as regularize does after its own
+    search (regularize.py:192-196): weight x g, su / g."""
+    from .gss import g_scale_search_batch, sample_scale_tiles
+    results = g_scale_search_batch([sample_scale_tiles(pm.reg.weight) for pm in prepared],
+                                   tile_encoder)
+    for pm, (g, _) in zip(prepared, results):
+        g = float(g)
+        if not g > 0.0:
+            raise ValueError(f"global-scale search returned a non-positive scale: {g}")
+        pm.reg.weight.mul_(g)
+        pm.reg.su.div_(g)
+        pm.reg.g_scale = g
+
+
 def _finish_module(pm: _PreparedModule, lq: LDLQResult, K: int, cb: int,
                    shared_seconds: float) -> QuantizedModuleResult:
     """Back to the original basis and the metrics (layer_quant.py:216-265);
@@ -331,10 +347,17 @@ def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Ten
     try:
         if lockstep:
             tp = time.time()
+            # The global-scale search of every projection runs as one batch
+            # after their regularisation (two encoder stages for the layer
+            # instead of two per projection); each projection's scale equals
+            # its own search's, since a candidate's MSE depends on its tiles
+            # only.
             prepared = [_prepare_module(name, available[name].weight.data,
                                         device_h[id(hessians[name])], K, cb, encoder,
-                                        skip_g_scale, block_size, ldl_cache)
+                                        True, block_size, ldl_cache)
                         for name in selected]
+            if not skip_g_scale:
+                _apply_global_scales(prepared, encoder)
             torch.cuda.synchronize(device)
             t0 = time.time()
             lqs = ldlq_lockstep([(pm.reg.weight, pm.ldl.transformed) for pm in prepared],

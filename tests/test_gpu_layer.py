@@ -219,3 +219,38 @@ def test_decoder_layer_two_lanes_equal_sequential(torch_mod):
         assert torch.equal(r.encoded, seq.module_results[name].encoded), name
         assert torch.equal(r.w_hat, seq.module_results[name].w_hat), name
     assert 0 < rep.encoder_seconds <= rep.extra["traversal_seconds"] * 1.05
+
+
+def test_decoder_layer_batched_global_scale_search(torch_mod):
+    """With the global-scale search on (skip_g_scale=False), lockstep runs
+    one batched search for all projections (gss.py:118-184 over every
+    projection's sample at once); each projection's scale, states and
+    reconstruction equal its own search in the one-at-a-time order."""
+    from exl3_intel_arc_quantizer_amd.layer_quant import (hessian_from_activations,
+                                                          quantize_decoder_layer)
+    torch = torch_mod
+    nn = torch.nn
+    torch.manual_seed(2)
+    layer = nn.Module()
+    layer.self_attn = nn.Module()
+    layer.mlp = nn.Module()
+    layer.self_attn.q_proj = nn.Linear(256, 256, bias=False)
+    layer.mlp.up_proj = nn.Linear(256, 384, bias=False)
+    layer.mlp.down_proj = nn.Linear(384, 256, bias=False)
+    layer = layer.cuda()
+    with torch.no_grad():
+        layer.mlp.up_proj.weight.mul_(7.0)
+    rng = np.random.default_rng(32)
+    h256, _ = hessian_from_activations(
+        torch.from_numpy(rng.standard_normal((1024, 256)).astype(np.float32)).cuda())
+    h384, _ = hessian_from_activations(
+        torch.from_numpy(rng.standard_normal((1024, 384)).astype(np.float32)).cuda())
+    hess = {"self_attn.q_proj": h256, "mlp.up_proj": h256, "mlp.down_proj": h384}
+    rep = quantize_decoder_layer(layer, hess, K=2, skip_g_scale=False)
+    seq = quantize_decoder_layer(layer, hess, K=2, skip_g_scale=False, lockstep=False)
+    for name, r in rep.module_results.items():
+        s = seq.module_results[name]
+        assert r.metrics.g_scale == s.metrics.g_scale and r.metrics.g_scale != 1.0, name
+        assert torch.equal(r.su, s.su), name
+        assert torch.equal(r.encoded, s.encoded), name
+        assert torch.equal(r.w_hat, s.w_hat), name
