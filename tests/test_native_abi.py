@@ -166,3 +166,42 @@ def test_traceback_policy_switch():
     assert _native.set_traceback_policy("auto") == "stream"
     with pytest.raises(ValueError):
         _native.set_traceback_policy("fast")
+
+
+def test_layer_entry_points_reject_bad_arguments():
+    """include/exl3_layer.h: every argument check runs on the host, before
+    any launch (dummy non-NULL pointers never reach a kernel here)."""
+    lib = _native.load_library()
+    err = lambda: lib.exl3_last_error().decode()  # noqa: E731
+    assert lib.exl3_hadamard128(None, None, 128, 128, 0, None) != 0 and "NULL" in err()
+    assert lib.exl3_hadamard128(1, 1, 100, 128, 0, None) != 0 and "divisible by 128" in err()
+    assert lib.exl3_hadamard128(1, 1, 128, 100, 1, None) != 0 and "divisible by 128" in err()
+    assert lib.exl3_hadamard128(1, 1, 128, 128, 2, None) != 0 and "side" in err()
+    assert lib.exl3_hadamard128(1, 1, 0, 128, 0, None) != 0 and "empty" in err()
+    assert lib.exl3_block_rms_workspace(256, 384, 0, 32) == 384 * 8
+    assert lib.exl3_block_rms_workspace(100, 70, 1, 32) == 100 * 3
+    assert lib.exl3_block_rms_workspace(100, 70, 2, 32) == -1
+    assert lib.exl3_block_rms(1, 1, 100, 70, 1, 32, 1, 299, None) != 0 and "workspace" in err()
+    assert lib.exl3_block_rms(1, 1, 100, 70, 3, 32, 1, 10 ** 6, None) != 0 and "dim" in err()
+    assert lib.exl3_block_rms(1, 1, 100, 70, 0, 0, 1, 10 ** 6, None) != 0 and "blocksize" in err()
+    assert lib.exl3_block_rms(1, 1, 100, 70, 0, 32, None, 10 ** 6, None) != 0 and "NULL" in err()
+    assert lib.exl3_cholesky_block_order() == 128
+    assert lib.exl3_cholesky_diag_block(1, 256, 0, 0, 1, None) != 0 and "order" in err()
+    assert lib.exl3_cholesky_diag_block(1, 256, 129, 0, 1, None) != 0 and "order" in err()
+    assert lib.exl3_cholesky_diag_block(1, 64, 128, 0, 1, None) != 0 and "lda" in err()
+    assert lib.exl3_cholesky_diag_block(1, 256, 128, -1, 1, None) != 0 and "offset" in err()
+    assert lib.exl3_cholesky_diag_block(1, 256, 128, 0, None, None) != 0 and "NULL" in err()
+    assert lib.exl3_ldlq_gather(1, 0, 16, 1, None) != 0 and "no blocks" in err()
+    assert lib.exl3_ldlq_gather(1, 1, 0, 1, None) != 0 and "tile count" in err()
+    assert lib.exl3_ldlq_gather(None, 1, 16, 1, None) != 0 and "NULL" in err()
+    assert lib.exl3_ldlq_scatter(1, 1, 16, 1, None, None) != 0 and "NULL" in err()
+    assert lib.exl3_ldlq_scatter(1, 1, -3, 1, 1, None) != 0 and "tile count" in err()
+
+
+def test_ldlq_block_table_fields_match_the_header():
+    """_native.LDLQ_BLOCK_FIELDS lists exl3_ldlq_block's int64 fields in the
+    header's order (the ldlq driver builds the table row by row)."""
+    text = (REPO_ROOT / "include" / "exl3_layer.h").read_text()
+    body = text[text.index("typedef struct exl3_ldlq_block {"):text.index("} exl3_ldlq_block;")]
+    fields = re.findall(r"int64_t (\w+);", body)
+    assert tuple(fields) == _native.LDLQ_BLOCK_FIELDS
