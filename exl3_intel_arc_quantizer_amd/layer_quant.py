@@ -46,13 +46,25 @@ def hessian_from_activations(x: torch.Tensor, damping_lambda: float = DEFAULT_DA
     """Hessian of one projection input: sum over token chunks of X^T X in
     float32 (calibration.py:337-352), divided by the token count, diagonal
     damped by lambda * mean(diag) and floored at ``zero_floor``
-    (calibration.py:359-385). Returns (H, applied damping)."""
+    (calibration.py:359-385). Returns (H, applied damping).
+
+    bf16 / fp16 activations on the GPU go straight into a half-precision
+    GEMM with float32 output (``torch.mm(..., out_dtype=float32)``, MFMA
+    with fp32 accumulation): their products are exact in float32, so the
+    result is the float32 GEMM of the converted values up to summation
+    order, without the conversion pass and at the half-precision MFMA
+    rate."""
     d = x.shape[-1]
     flat = x.reshape(-1, d)
     H = torch.zeros((d, d), dtype=torch.float32, device=x.device)
+    half = flat.device.type == "cuda" and flat.dtype in (torch.bfloat16, torch.float16)
     for s in range(0, flat.shape[0], chunk_tokens):
-        xf = flat[s:s + chunk_tokens].to(torch.float32)
-        H += xf.T @ xf
+        if half:
+            xc = flat[s:s + chunk_tokens]
+            H += torch.mm(xc.T, xc, out_dtype=torch.float32)
+        else:
+            xf = flat[s:s + chunk_tokens].to(torch.float32)
+            H += xf.T @ xf
     H /= max(1, flat.shape[0])
     diag = H.diagonal()
     damp = max(1e-8, damping_lambda * diag.mean().item())
