@@ -254,3 +254,42 @@ def test_decoder_layer_batched_global_scale_search(torch_mod):
         assert torch.equal(r.su, s.su), name
         assert torch.equal(r.encoded, s.encoded), name
         assert torch.equal(r.w_hat, s.w_hat), name
+
+
+def test_ldlq_hip_encoder_equals_cpu_encoder(torch_mod):
+    """tests/test_ldlq_loop.py:380-392: one LDLQ traversal on the GPU run once
+    with the HIP tile encoder and once with the CPU encoder (the C oracle
+    behind the same adapter contract) gives equal Wq and states, alone and
+    in lockstep (where the HIP adapter runs two lanes on two streams and
+    the plain CPU callable one)."""
+    from exl3_intel_arc_quantizer_amd.ldlq import block_ldl, ldlq, ldlq_lockstep
+    from exl3_intel_arc_quantizer_amd.tile_encoder import make_xpu_tile_encoder
+    from oracle import c_oracle
+    torch = torch_mod
+    rng = np.random.default_rng(51)
+
+    def problem(k, n, seed):
+        _, X = _layer_case(k, n, seed)
+        Xc = torch.from_numpy(X).cuda()
+        L = block_ldl((Xc.T @ Xc) / X.shape[0] + 0.05 * torch.eye(k, device="cuda")).transformed
+        W = torch.from_numpy((rng.standard_normal((k, n)) * 0.5).astype(np.float32)).cuda()
+        return W, L
+
+    def cpu_encoder(tiles):
+        t16 = tiles.detach().cpu().numpy().astype(np.float16).astype(np.float32)
+        r = c_oracle.encode_tiles(t16, K=2, cb=2, pre_permute=False)
+        return (torch.from_numpy(r.reconstructed_perm.astype(np.float32)).to(tiles.device),
+                torch.from_numpy(r.output_indices.view(np.int16).copy()).to(tiles.device))
+
+    hip = make_xpu_tile_encoder(K=2)
+    try:
+        W, L = problem(256, 256, 52)
+        a, b = ldlq(W, L, hip), ldlq(W, L, cpu_encoder)
+        assert torch.equal(a.weight_q, b.weight_q) and torch.equal(a.encoded, b.encoded)
+        probs = [problem(256, 128, 53), problem(384, 256, 54)]
+        got = ldlq_lockstep(probs, hip)
+        want = ldlq_lockstep(probs, cpu_encoder)
+        for g, w in zip(got, want):
+            assert torch.equal(g.weight_q, w.weight_q) and torch.equal(g.encoded, w.encoded)
+    finally:
+        hip.encoder.arena.release()
