@@ -83,9 +83,11 @@ __device__ __forceinline__ uint16_t bits_f16(f16 h) { return __builtin_bit_cast(
 __device__ __forceinline__ f16 decode_state(int cb, uint32_t s) {
   if (cb == 2) {
     const uint32_t x = s * 0x83DCD12Du;
-    const uint32_t bsum = (x & 0xFFu) + ((x >> 8) & 0xFFu) + ((x >> 16) & 0xFFu) + (x >> 24);
-    // 0x6400 + bsum is the fp16 encoding of 1024 + bsum; one fused fp16 FMA.
-    return __builtin_fmaf16(f16_bits(0x6400u + bsum), f16_bits(0x1EEEu), f16_bits(0xC931u));
+    // v_sad_u8(x, 0, 0x6400) = 0x6400 + the sum of x's four bytes (each
+    // |byte - 0|) in one instruction; 0x6400 + bsum is the fp16 encoding of
+    // 1024 + bsum (bsum <= 1020). One fused fp16 FMA.
+    const uint32_t h = __builtin_amdgcn_sad_u8(x, 0u, 0x6400u);
+    return __builtin_fmaf16(f16_bits(h), f16_bits(0x1EEEu), f16_bits(0xC931u));
   }
   uint32_t x = (cb == 0) ? (s * 89226354u + 64248484u) : (s * 0xCBAC1FEDu);
   x = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
