@@ -953,6 +953,7 @@ __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
   constexpr int KR = 16 - K;
   constexpr int STRIDE = exl3::row_stride(K);
   __shared__ uint16_t s_wbits[256];  // the tile's fp16 inputs, ring order
+  __shared__ uint16_t s_oidx[256];   // the walk's states, ring order (write pass)
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   const int L = a.L;
@@ -983,10 +984,7 @@ __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
         int rj = i + a.roll;
         if (rj >= L) rj -= L;
         const uint32_t sigma = (((ks >> (K * j)) & ((1u << K) - 1u)) << KR) | edge;
-        if (a.write && lane == 0) {
-          a.out_idx[(int64_t)t * L + rj] = (int16_t)(uint16_t)sigma;
-          a.out_w[(int64_t)t * L + rj] = (float)decode_state(CB, sigma);
-        }
+        if (a.write && lane == 0) s_oidx[rj] = (uint16_t)sigma;
         edge = sigma >> K;
         --i;
       }
@@ -997,13 +995,21 @@ __global__ void __launch_bounds__(64) traceback_rows_kernel(TbArgs a) {
     if (ri >= L) ri -= L;
     const uint32_t k = tb_branch<K, CB, 0, true>(nullptr, edge, wbits, ri, L, lane, pre);
     const uint32_t sigma = (k << KR) | edge;
-    if (a.write && lane == 0) {
-      a.out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
-      a.out_w[(int64_t)t * L + ri] = (float)decode_state(CB, sigma);
-    }
+    if (a.write && lane == 0) s_oidx[ri] = (uint16_t)sigma;
     edge = sigma >> K;
   }
-  if (!a.write && lane == 0) a.end_out[(int64_t)t * a.end_stride] = (int32_t)edge;
+  if (a.write) {
+    // The states and their codebook values leave after the walk, coalesced
+    // over the wave, so the serial walk carries no decode or global store.
+    __syncthreads();
+    for (int r = lane; r < L; r += 64) {
+      const uint32_t sigma = s_oidx[r];
+      a.out_idx[(int64_t)t * L + r] = (int16_t)(uint16_t)sigma;
+      a.out_w[(int64_t)t * L + r] = (float)decode_state(CB, sigma);
+    }
+  } else if (lane == 0) {
+    a.end_out[(int64_t)t * a.end_stride] = (int32_t)edge;
+  }
 }
 
 // Streamed cost-row traceback for small batches. The traceback above is
@@ -1045,7 +1051,6 @@ __global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kern
   __shared__ u32x4 s_ring[2][RV];
   __shared__ uint16_t s_wbits[256];
   __shared__ uint16_t s_oidx[256];
-  __shared__ float s_ow[256];
   const int t = blockIdx.x;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -1108,10 +1113,7 @@ __global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kern
             int rj = i + roll;
             if (rj >= L) rj -= L;
             const uint32_t sigma = (((ks >> (K * j)) & ((1u << K) - 1u)) << KR) | edge;
-            if (a.write && lane == 0) {
-              s_oidx[rj] = (uint16_t)sigma;
-              s_ow[rj] = (float)decode_state(CB, sigma);
-            }
+            if (a.write && lane == 0) s_oidx[rj] = (uint16_t)sigma;
             edge = sigma >> K;
             --i;
           }
@@ -1138,17 +1140,15 @@ __global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kern
     if (ri >= L) ri -= L;
     const uint32_t k = tb_branch<K, CB, 0, true>(nullptr, edge, wbits, ri, L, lane, pre);
     const uint32_t sigma = (k << KR) | edge;
-    if (a.write && lane == 0) {
-      s_oidx[ri] = (uint16_t)sigma;
-      s_ow[ri] = (float)decode_state(CB, sigma);
-    }
+    if (a.write && lane == 0) s_oidx[ri] = (uint16_t)sigma;
     edge = sigma >> K;
   }
   if (a.write) {
     __builtin_amdgcn_wave_barrier();
     for (int r = lane; r < L; r += 64) {
-      a.out_idx[(int64_t)t * L + r] = (int16_t)s_oidx[r];
-      a.out_w[(int64_t)t * L + r] = s_ow[r];
+      const uint32_t sigma = s_oidx[r];
+      a.out_idx[(int64_t)t * L + r] = (int16_t)(uint16_t)sigma;
+      a.out_w[(int64_t)t * L + r] = (float)decode_state(CB, sigma);
     }
   } else if (lane == 0) {
     a.end_out[(int64_t)t * a.end_stride] = (int32_t)edge;
