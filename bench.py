@@ -171,11 +171,16 @@ def cpu_baseline_numpy(tiles, K, cores):
     import multiprocessing as mp
     n = 4 * cores
     ctx = mp.get_context("fork")
-    with ctx.Pool(cores) as pool:
+    pool = ctx.Pool(cores)
+    try:
         pool.map(_numpy_encode_one, [(tiles[0], K)] * cores)       # imports, warm
         t0 = time.perf_counter()
         pool.map(_numpy_encode_one, [(tiles[i], K) for i in range(n)], chunksize=1)
         dt = time.perf_counter() - t0
+    finally:
+        # Let the workers exit and reap them, so none outlives the benchmark.
+        pool.close()
+        pool.join()
     return {"value": round(n / dt, 3), "unit": "tiles/s", "cores": cores, "kind": "port",
             "sample": f"first {n} tiles of the benchmark matrix at K={K} ({dt:.1f} s, numpy "
                       "restatement of reference_encoder.py, one process per core)"}

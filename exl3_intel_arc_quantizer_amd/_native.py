@@ -46,6 +46,9 @@ _SIGNATURES = {
     "exl3_probe_hfma": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
     # include/exl3_layer.h
     "exl3_hadamard128": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_vp]),
+    "exl3_hadamard128_scaled": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_vp, _c_vp,
+                                         _c_vp]),
+    "exl3_block_rms_from_slices": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
     "exl3_block_rms": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_i64,
                                 _c_vp]),
     "exl3_block_rms_workspace": (_c_i64, [_c_i64, _c_i64, _c_int, _c_int]),
@@ -469,6 +472,49 @@ def hadamard128(x, out, side: int) -> None:
                                                int(side), _stream(dev)), "hadamard128")
 
 
+def hadamard128_scaled(x, out, side: int, divisor=None, slice_sumsq=None) -> None:
+    """``out = (x / divisor[col]) @ H`` per 128-column block (side 1) or
+    ``out = H @ (x / divisor[row])`` per 128-row block (side 0); with side 1
+    ``slice_sumsq`` (rows x cols / 32 float32) receives the sums of squares
+    of every 32-element slice of the output rows. ``out`` may be ``x``."""
+    torch = _torch()
+    dev = _matrix(x, "x")
+    _check_buffer(out, "out", x.dtype, tuple(x.shape), dev)
+    rows, cols = x.shape
+    if divisor is not None:
+        want = cols if side == 1 else rows
+        if (not isinstance(divisor, torch.Tensor) or divisor.dtype != torch.float32
+                or not divisor.is_contiguous() or divisor.device != x.device
+                or divisor.numel() != want):
+            raise RuntimeError(f"divisor must be a contiguous float32 tensor of {want} elements "
+                               f"on {x.device}")
+    if slice_sumsq is not None:
+        if side != 1 or cols % 32:
+            raise RuntimeError("slice sums of squares need side 1 and columns divisible by 32")
+        _check_buffer(slice_sumsq, "slice_sumsq", torch.float32, (rows, cols // 32), dev)
+    with torch.cuda.device(dev):
+        _check(load_library().exl3_hadamard128_scaled(
+            x.data_ptr(), out.data_ptr(), rows, cols, int(side),
+            divisor.data_ptr() if divisor is not None else None,
+            slice_sumsq.data_ptr() if slice_sumsq is not None else None, _stream(dev)),
+            "hadamard128_scaled")
+
+
+def block_rms_from_slices(slice_sumsq, out, n: int) -> None:
+    """``out[o] = sqrt(sum_s slice_sumsq[o, s] / n)``, the slices added in
+    order (the second pass of block_rms)."""
+    torch = _torch()
+    dev = _matrix(slice_sumsq, "slice_sumsq")
+    outputs, slices = slice_sumsq.shape
+    if (not isinstance(out, torch.Tensor) or out.dtype != torch.float32 or not out.is_contiguous()
+            or out.device != slice_sumsq.device or out.numel() != outputs):
+        raise RuntimeError(f"out must be a contiguous float32 tensor of {outputs} elements")
+    with torch.cuda.device(dev):
+        _check(load_library().exl3_block_rms_from_slices(slice_sumsq.data_ptr(), out.data_ptr(),
+                                                         outputs, int(n), slices, _stream(dev)),
+               "block_rms_from_slices")
+
+
 def block_rms(x, out, dim: int, blocksize: int = 32) -> None:
     """regularize.py:41-56 into ``out`` (``x.shape[1 - dim]`` elements,
     any shape)."""
@@ -516,6 +562,30 @@ def cholesky_diag_block(a, j0: int, nb: int, info) -> None:
 
 
 LDLQ_BLOCK_FIELDS = ("w", "comp", "wq", "err", "states", "n", "tile0", "reserved")
+
+
+def check_ldlq_rows(rows, tiles: int) -> None:
+    """Host check of one encoder call's ``exl3_ldlq_block`` rows before they
+    are uploaded: every block's n is a positive multiple of 16, the first
+    block starts at batch tile 0, each next one where the previous ends, and
+    together they cover exactly ``tiles`` tiles. The kernels trust the table
+    for their addresses, so a table that breaks this is refused here."""
+    import numpy as np
+    r = np.asarray(rows, dtype=np.int64).reshape(-1, len(LDLQ_BLOCK_FIELDS))
+    if r.shape[0] < 1:
+        raise ValueError("an LDLQ call needs at least one block")
+    n = r[:, LDLQ_BLOCK_FIELDS.index("n")]
+    tile0 = r[:, LDLQ_BLOCK_FIELDS.index("tile0")]
+    if (n <= 0).any() or (n % 16).any():
+        raise ValueError(f"block widths must be positive multiples of 16, got {n.tolist()}")
+    ends = np.cumsum(n // 16)
+    starts = np.concatenate([[0], ends[:-1]])
+    if not np.array_equal(tile0, starts) or int(ends[-1]) != int(tiles):
+        raise ValueError(f"blocks must tile the batch back to back from 0 to {tiles}: tile0 "
+                         f"{tile0.tolist()}, widths {(n // 16).tolist()}")
+    for field in ("w", "comp", "wq", "err", "states"):
+        if (r[:, LDLQ_BLOCK_FIELDS.index(field)] == 0).any():
+            raise ValueError(f"NULL {field} address in an LDLQ block row")
 
 
 def _ldlq_table(table, tiles_like, name: str) -> tuple:

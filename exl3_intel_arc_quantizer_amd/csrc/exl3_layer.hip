@@ -56,33 +56,63 @@ __device__ __forceinline__ float had_level(float v, int lane, int h) {
   return (lane & h) ? p - v : v + p;
 }
 
+// DIV: every element of column c is divided by div[c] before the transform
+// (regularize's fold of sv into the weight). SUMSQ: the sum of squares of
+// each 32-element slice of the transformed row goes to
+// sumsq[row * (cols / 32) + slice] (the first pass of the row RMS that
+// follows the transform); lanes 16 j .. 16 j + 15 hold slice j of the
+// segment and add their squares in a butterfly.
+template <bool DIV, bool SUMSQ>
 __global__ void __launch_bounds__(64 * HAD_RIGHT_WAVES)
-    had128_right_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t segments) {
+    had128_right_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t segments,
+                        int64_t seg_per_row, const float* __restrict__ div,
+                        float* __restrict__ sumsq) {
   const int lane = threadIdx.x & 63;
   const int64_t stride = (int64_t)gridDim.x * HAD_RIGHT_WAVES;
   for (int64_t seg = (int64_t)blockIdx.x * HAD_RIGHT_WAVES + (threadIdx.x >> 6); seg < segments;
        seg += stride) {
     // Lane l holds elements 2l and 2l + 1 of the segment.
-    const float2 v = reinterpret_cast<const float2*>(in + seg * HAD_N)[lane];
+    float2 v = reinterpret_cast<const float2*>(in + seg * HAD_N)[lane];
+    if (DIV) {
+      const float2 d =
+          reinterpret_cast<const float2*>(div + (seg % seg_per_row) * HAD_N)[lane];
+      v.x = v.x / d.x;
+      v.y = v.y / d.y;
+    }
     float lo = v.x + v.y, hi = v.x - v.y;
 #pragma unroll
     for (int h = 1; h < 64; h <<= 1) {
       lo = had_level(lo, lane, h);
       hi = had_level(hi, lane, h);
     }
-    reinterpret_cast<float2*>(out + seg * HAD_N)[lane] = make_float2(lo * kHadScale,
-                                                                     hi * kHadScale);
+    lo = lo * kHadScale;
+    hi = hi * kHadScale;
+    reinterpret_cast<float2*>(out + seg * HAD_N)[lane] = make_float2(lo, hi);
+    if (SUMSQ) {
+      float q = lo * lo + hi * hi;
+#pragma unroll
+      for (int h = 1; h < 16; h <<= 1) q = q + __shfl_xor(q, h, 64);
+      if ((lane & 15) == 0) sumsq[seg * (HAD_N / 32) + (lane >> 4)] = q;
+    }
   }
 }
 
+// DIV: every element of row r is divided by div[r] before the transform
+// (the fold of su).
+template <bool DIV>
 __global__ void __launch_bounds__(256)
-    had128_left_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t cols) {
+    had128_left_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t cols,
+                       const float* __restrict__ div) {
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (c >= cols) return;
-  const int64_t base = (int64_t)blockIdx.y * HAD_N * cols + c;
+  const int64_t row0 = (int64_t)blockIdx.y * HAD_N;
+  const int64_t base = row0 * cols + c;
   float v[HAD_N];
 #pragma unroll
-  for (int r = 0; r < HAD_N; ++r) v[r] = in[base + r * cols];
+  for (int r = 0; r < HAD_N; ++r) {
+    v[r] = in[base + r * cols];
+    if (DIV) v[r] = v[r] / div[row0 + r];
+  }
 #pragma unroll
   for (int h = 1; h < HAD_N; h <<= 1) {
 #pragma unroll
@@ -255,9 +285,13 @@ __global__ void __launch_bounds__(256)
                        float* __restrict__ x) {
   const int64_t tile = blockIdx.x;
   const exl3_ldlq_block blk = blocks[ldlq_block_of(blocks, nblocks, tile)];
+  const int64_t t = tile - blk.tile0;
+  // A table that does not cover this tile writes nothing (the host checks
+  // the table before it is uploaded).
+  if (t < 0 || t >= blk.n / 16) return;
   const int p = threadIdx.x;
   const int e = exl3::tc_perm(p);
-  const int64_t off = (int64_t)(e >> 4) * blk.n + (tile - blk.tile0) * 16 + (e & 15);
+  const int64_t off = (int64_t)(e >> 4) * blk.n + t * 16 + (e & 15);
   const float* w = reinterpret_cast<const float*>(blk.w);
   const float* comp = reinterpret_cast<const float*>(blk.comp);
   x[tile * 256 + p] = w[off] + comp[off];
@@ -268,15 +302,60 @@ __global__ void __launch_bounds__(256)
                         const float* __restrict__ recon, const int16_t* __restrict__ idx) {
   const int64_t tile = blockIdx.x;
   const exl3_ldlq_block blk = blocks[ldlq_block_of(blocks, nblocks, tile)];
+  const int64_t t = tile - blk.tile0;
+  if (t < 0 || t >= blk.n / 16) return;
   const int p = threadIdx.x;
   const int e = exl3::tc_perm(p);
-  const int64_t t = tile - blk.tile0;
   const int64_t off = (int64_t)(e >> 4) * blk.n + t * 16 + (e & 15);
   const float v = recon[tile * 256 + p];
   const float w = reinterpret_cast<const float*>(blk.w)[off];
   reinterpret_cast<float*>(blk.wq)[off] = v;
   reinterpret_cast<float*>(blk.err)[off] = w - v;
   reinterpret_cast<int16_t*>(blk.states)[t * 256 + p] = idx[tile * 256 + p];
+}
+
+// Checks the shape and launches the Hadamard kernel variant for (side,
+// divisor present, sums of squares wanted).
+int launch_hadamard(const float* in, float* out, int64_t rows, int64_t cols, int side,
+                    const float* div, float* sumsq, void* stream, const char* what) {
+  if (!in || !out) return set_error("%s: NULL buffer", what);
+  if (rows <= 0 || cols <= 0) return set_error("%s: empty matrix (%lld x %lld)", what,
+                                                (long long)rows, (long long)cols);
+  if (side != 0 && side != 1) return set_error("%s: side must be 0 or 1, got %d", what, side);
+  if (side == 0 && rows % HAD_N)
+    return set_error("%s: rows (%lld) must be divisible by 128", what, (long long)rows);
+  if (side == 1 && cols % HAD_N)
+    return set_error("%s: columns (%lld) must be divisible by 128", what, (long long)cols);
+  hipStream_t st = as_stream(stream);
+  if (side == 1) {
+    const int64_t seg_per_row = cols / HAD_N;
+    const int64_t segments = rows * seg_per_row;
+    const int64_t want = (segments + HAD_RIGHT_WAVES - 1) / HAD_RIGHT_WAVES;
+    // Grid-stride beyond 65536 workgroups (several segments per wave).
+    const int64_t blocks = want < 65536 ? want : 65536;
+    const dim3 grid((unsigned)blocks), block(64 * HAD_RIGHT_WAVES);
+    if (div && sumsq)
+      hipLaunchKernelGGL((had128_right_kernel<true, true>), grid, block, 0, st, in, out, segments,
+                         seg_per_row, div, sumsq);
+    else if (div)
+      hipLaunchKernelGGL((had128_right_kernel<true, false>), grid, block, 0, st, in, out,
+                         segments, seg_per_row, div, sumsq);
+    else if (sumsq)
+      hipLaunchKernelGGL((had128_right_kernel<false, true>), grid, block, 0, st, in, out,
+                         segments, seg_per_row, div, sumsq);
+    else
+      hipLaunchKernelGGL((had128_right_kernel<false, false>), grid, block, 0, st, in, out,
+                         segments, seg_per_row, div, sumsq);
+  } else {
+    const int64_t gx = (cols + 255) / 256, gy = rows / HAD_N;
+    if (gx > INT32_MAX || gy > 65535) return set_error("%s: matrix too large", what);
+    const dim3 grid((unsigned)gx, (unsigned)gy), block(256);
+    if (div)
+      hipLaunchKernelGGL((had128_left_kernel<true>), grid, block, 0, st, in, out, cols, div);
+    else
+      hipLaunchKernelGGL((had128_left_kernel<false>), grid, block, 0, st, in, out, cols, div);
+  }
+  return check_launch(what);
 }
 
 }  // namespace
@@ -287,30 +366,28 @@ extern "C" {
 
 int exl3_hadamard128(const float* in, float* out, int64_t rows, int64_t cols, int side,
                      void* stream) {
-  if (!in || !out) return set_error("hadamard128: NULL buffer");
-  if (rows <= 0 || cols <= 0) return set_error("hadamard128: empty matrix (%lld x %lld)",
-                                                (long long)rows, (long long)cols);
-  if (side != 0 && side != 1) return set_error("hadamard128: side must be 0 or 1, got %d", side);
-  if (side == 0 && rows % HAD_N)
-    return set_error("hadamard128: rows (%lld) must be divisible by 128", (long long)rows);
-  if (side == 1 && cols % HAD_N)
-    return set_error("hadamard128: columns (%lld) must be divisible by 128", (long long)cols);
-  hipStream_t st = as_stream(stream);
-  if (side == 1) {
-    const int64_t segments = rows * (cols / HAD_N);
-    const int64_t want = (segments + HAD_RIGHT_WAVES - 1) / HAD_RIGHT_WAVES;
-    // Grid-stride beyond 65536 workgroups (several segments per wave).
-    const int64_t blocks = want < 65536 ? want : 65536;
-    if (blocks > INT32_MAX) return set_error("hadamard128: matrix too large");
-    hipLaunchKernelGGL(had128_right_kernel, dim3((unsigned)blocks), dim3(64 * HAD_RIGHT_WAVES), 0,
-                       st, in, out, segments);
-  } else {
-    const int64_t gx = (cols + 255) / 256, gy = rows / HAD_N;
-    if (gx > INT32_MAX || gy > 65535) return set_error("hadamard128: matrix too large");
-    hipLaunchKernelGGL(had128_left_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, st, in,
-                       out, cols);
-  }
-  return check_launch("hadamard128");
+  return launch_hadamard(in, out, rows, cols, side, nullptr, nullptr, stream, "hadamard128");
+}
+
+int exl3_hadamard128_scaled(const float* in, float* out, int64_t rows, int64_t cols, int side,
+                            const float* divisor, float* slice_sumsq, void* stream) {
+  if (slice_sumsq && side != 1)
+    return set_error("hadamard128_scaled: slice sums of squares need side = 1");
+  return launch_hadamard(in, out, rows, cols, side, divisor, slice_sumsq, stream,
+                         "hadamard128_scaled");
+}
+
+int exl3_block_rms_from_slices(const float* slice_sumsq, float* out, int64_t outputs, int64_t n,
+                               int64_t slices, void* stream) {
+  if (!slice_sumsq || !out) return set_error("block_rms_from_slices: NULL buffer");
+  if (outputs <= 0 || n <= 0 || slices <= 0)
+    return set_error("block_rms_from_slices: empty shape (%lld outputs, n %lld, %lld slices)",
+                     (long long)outputs, (long long)n, (long long)slices);
+  unsigned b;
+  if (exl3::grid_1d(outputs, 256, &b, "block_rms_from_slices")) return 1;
+  hipLaunchKernelGGL(block_rms_reduce_kernel, dim3(b), dim3(256), 0, as_stream(stream),
+                     slice_sumsq, out, outputs, n, slices, 1);
+  return check_launch("block_rms_from_slices");
 }
 
 int64_t exl3_block_rms_workspace(int64_t rows, int64_t cols, int dim, int blocksize) {

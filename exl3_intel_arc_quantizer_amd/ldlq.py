@@ -317,6 +317,7 @@ def _block_table(walks: List[_Traversal], steps: List[List[Tuple[int, int]]]):
         for t in (w.weight, w.prod_cache, w.weight_q, w.err, w.encoded):
             if not t.is_contiguous():
                 raise ValueError("LDLQ buffers must be contiguous")
+    from ._native import check_ldlq_rows
     rows, spans = [], []
     for call in steps:
         tile0 = 0
@@ -324,6 +325,7 @@ def _block_table(walks: List[_Traversal], steps: List[List[Tuple[int, int]]]):
         for w, b in call:
             rows.append(walks[w].block_row(b, tile0))
             tile0 += walks[w].tiles_n
+        check_ldlq_rows(rows[first:], tile0)
         spans.append((first, len(call), tile0))
     table = torch.from_numpy(np.asarray(rows, dtype=np.int64)).to(walks[0].weight.device)
     return table, spans

@@ -1,28 +1,47 @@
-"""Reserve-based admission policy for encoder scratch on a discrete MI355X.
+"""Admission control for encoder scratch in a discrete GPU's HBM.
 
-Counterpart of exl3_quant/memory_policy.py:194-421 with the same names
+Public names follow the reference's exl3_quant/memory_policy.py:194-421
 (``MemorySnapshot``, ``capture_snapshot``, ``MemoryPressureError``,
-``MemoryPolicy``, env overrides). What changes for 288 GB of dedicated HBM3E:
+``MemoryPolicy`` and the environment switches), so arena code and scripts
+written against it keep working. The model behind them is this build's own.
 
-* the binding figure is the device's free HBM (``torch.cuda.mem_get_info``);
-  host RAM is a separate pool and no longer the tighter of two overlapping
-  counters (the reference's integrated-GPU rule, memory_policy.py:210-215);
-* the device counters fall when the process commits memory, so by default the
-  live allocation is *not* subtracted a second time
-  (``reflect_outstanding`` defaults to True; ``EXL3_MEMORY_REFLECT_OUTSTANDING=0``
-  restores the reference's subtraction);
-* the default reserve is 8 GiB (``EXL3_MEMORY_RESERVE_GIB`` /
-  ``EXL3_MEMORY_RESERVE_BYTES`` override it, as in the reference).
+On an MI355X the scratch arena lives in the GPU's 288 GB of HBM3E, a pool
+that the host never shares. One figure therefore decides admission: the
+device's free HBM as the driver reports it (``hipMemGetInfo`` through
+``torch.cuda.mem_get_info``). Host RAM and swap are still recorded in
+every snapshot, because logs and scripts read them, but they never bind.
+On a host without a GPU the host's available RAM stands in for the device
+figure, so the same arithmetic can be tested on a CPU.
+
+A request is admitted when it fits into
+
+    admissible = free HBM - reserve - (outstanding, if counted)
+
+* The reserve is headroom that the encoder leaves for everything else in
+  the process: the layer driver's Hessians, GEMM workspaces, the caching
+  allocator's slack. The default is 8 GiB. ``EXL3_MEMORY_RESERVE_GIB``
+  (a float) or ``EXL3_MEMORY_RESERVE_BYTES`` (an integer) override it, and
+  the GiB form takes precedence.
+* The HBM counter already falls when this process commits memory, so by
+  default the caller's outstanding bytes are not subtracted a second time.
+  ``EXL3_MEMORY_REFLECT_OUTSTANDING=0`` subtracts them anyway, for drivers
+  whose counters lag behind the allocator.
+* An optional ceiling bounds any single buffer.
+
+After an allocation, ``check_after_commit`` confirms that the allocator
+really grew by the requested bytes and that free HBM did not sink below
+the reserve (minus a slack for counter noise).
 """
 
 from __future__ import annotations
 
+import dataclasses
 import os
 from dataclasses import dataclass, field
 from typing import Optional
 
-BYTES_PER_MIB = 1024 ** 2
-BYTES_PER_GIB = 1024 ** 3
+BYTES_PER_MIB = 1 << 20
+BYTES_PER_GIB = 1 << 30
 
 DEFAULT_RESERVE_BYTES = 8 * BYTES_PER_GIB
 DEFAULT_SAFETY_SLACK_BYTES = 256 * BYTES_PER_MIB
@@ -31,61 +50,80 @@ ENV_RESERVE_BYTES = "EXL3_MEMORY_RESERVE_BYTES"
 ENV_RESERVE_GIB = "EXL3_MEMORY_RESERVE_GIB"
 ENV_REFLECT_OUTSTANDING = "EXL3_MEMORY_REFLECT_OUTSTANDING"
 
-_MEMINFO_FIELDS = ("MemTotal", "MemFree", "MemAvailable", "Cached", "SwapTotal", "SwapFree",
-                   "SwapCached")
+# /proc/meminfo keys recorded in a snapshot (the file states them in kB).
+_HOST_KEYS = ("MemTotal", "MemFree", "MemAvailable", "Cached", "SwapTotal", "SwapFree",
+              "SwapCached")
+_FALSE_WORDS = frozenset(("0", "false", "no", "off"))
 
 
 def reflect_outstanding_counters() -> bool:
-    """True unless EXL3_MEMORY_REFLECT_OUTSTANDING is set to a false value."""
-    raw = os.environ.get(ENV_REFLECT_OUTSTANDING)
-    if raw is None or not raw.strip():
-        return True
-    return raw.strip().lower() in ("1", "true", "yes", "on")
+    """Whether the free-HBM counter already includes this process's live
+    allocations. True unless ``EXL3_MEMORY_REFLECT_OUTSTANDING`` is set to
+    0 / false / no / off."""
+    value = os.environ.get(ENV_REFLECT_OUTSTANDING, "").strip().lower()
+    return value not in _FALSE_WORDS
 
 
 def default_reserve_bytes() -> int:
-    """Configured reserve in bytes; the GiB form wins (memory_policy.py:78-92)."""
-    raw_gib = os.environ.get(ENV_RESERVE_GIB)
-    if raw_gib:
+    """The reserve from the environment (GiB form first, then bytes); an
+    unset or unparsable value falls through to the next source and finally
+    to DEFAULT_RESERVE_BYTES."""
+    sources = ((ENV_RESERVE_GIB, lambda s: int(float(s) * BYTES_PER_GIB)),
+               (ENV_RESERVE_BYTES, int))
+    for name, parse in sources:
+        text = os.environ.get(name)
+        if not text:
+            continue
         try:
-            return int(float(raw_gib) * BYTES_PER_GIB)
-        except (TypeError, ValueError):
-            pass
-    raw_bytes = os.environ.get(ENV_RESERVE_BYTES)
-    if raw_bytes:
-        try:
-            return int(raw_bytes)
-        except (TypeError, ValueError):
-            pass
+            return parse(text)
+        except ValueError:
+            continue
     return DEFAULT_RESERVE_BYTES
 
 
 def format_bytes(value: Optional[int]) -> str:
+    """Binary-unit rendering for messages: ``2.50 GiB``, ``12.0 MiB``, ``512 B``."""
     if value is None:
         return "n/a"
+    magnitude = abs(value)
     sign = "-" if value < 0 else ""
-    value = abs(value)
-    if value >= BYTES_PER_GIB:
-        return f"{sign}{value / BYTES_PER_GIB:.2f} GiB"
-    if value >= BYTES_PER_MIB:
-        return f"{sign}{value / BYTES_PER_MIB:.1f} MiB"
-    return f"{sign}{value} B"
+    for unit, size, digits in (("GiB", BYTES_PER_GIB, 2), ("MiB", BYTES_PER_MIB, 1)):
+        if magnitude >= size:
+            return f"{sign}{magnitude / size:.{digits}f} {unit}"
+    return f"{sign}{magnitude} B"
 
 
 def read_system_memory(path: str = "/proc/meminfo") -> dict:
-    """Parse a /proc/meminfo-style file into byte counts (missing fields = 0)."""
-    raw: dict = {}
+    """Host memory counters in bytes from a /proc/meminfo-style file; keys
+    the file lacks read as 0, keys this module does not record are dropped."""
+    found = {}
     with open(path, "r", encoding="ascii") as handle:
         for line in handle:
-            key, _, rest = line.partition(":")
-            if key in _MEMINFO_FIELDS:
-                raw[key] = int(rest.split()[0]) * 1024
-    return {name: raw.get(name, 0) for name in _MEMINFO_FIELDS}
+            key, sep, rest = line.partition(":")
+            if sep and key in _HOST_KEYS:
+                found[key] = int(rest.split()[0]) << 10
+    return {key: found.get(key, 0) for key in _HOST_KEYS}
+
+
+def read_system_memory_windows() -> dict:
+    """The reference reads host counters through GlobalMemoryStatusEx on
+    Windows. ROCm builds of this encoder run on Linux only."""
+    raise OSError("host memory counters through GlobalMemoryStatusEx exist on Windows only; "
+                  "this build reads /proc/meminfo")
+
+
+def read_system_memory_platform(meminfo_path: Optional[str] = None) -> dict:
+    """Host memory counters from ``meminfo_path`` or the platform's source
+    (/proc/meminfo on Linux)."""
+    if meminfo_path is None and os.name == "nt":  # pragma: no cover
+        return read_system_memory_windows()
+    return read_system_memory(meminfo_path or "/proc/meminfo")
 
 
 @dataclass(frozen=True)
 class MemorySnapshot:
-    """Host and device memory state at one point in time."""
+    """Memory counters at one instant. Device fields come from the HIP
+    runtime and torch's caching allocator, host fields from /proc/meminfo."""
 
     gpu_available: bool
     system_total_bytes: int
@@ -101,53 +139,50 @@ class MemorySnapshot:
 
     @property
     def binding_available_bytes(self) -> int:
-        """Free device HBM when a GPU is present, else host available memory."""
-        if self.gpu_available:
-            return self.device_free_bytes
-        return self.system_available_bytes
+        """The figure admission is decided on: free HBM on a GPU host (the
+        device's memory is its own pool), host available RAM otherwise."""
+        return self.device_free_bytes if self.gpu_available else self.system_available_bytes
 
     def as_dict(self) -> dict:
-        d = {name: getattr(self, name) for name in self.__dataclass_fields__}
-        d["binding_available_bytes"] = self.binding_available_bytes
-        return d
+        record = dataclasses.asdict(self)
+        record["binding_available_bytes"] = self.binding_available_bytes
+        return record
+
+
+def _device_counters(device_index: int):
+    """(free, total, allocated, reserved) bytes of one GPU, or None without one."""
+    try:
+        import torch
+        if not torch.cuda.is_available():
+            return None
+        free, total = torch.cuda.mem_get_info(device_index)
+        # One read of the allocator's statistics serves both counters.
+        stats = torch.cuda.memory_stats_as_nested_dict(device_index)
+        current = lambda name: int(stats.get(name, {}).get("all", {}).get("current", 0))  # noqa: E731
+        return int(free), int(total), current("allocated_bytes"), current("reserved_bytes")
+    except Exception:  # pragma: no cover - broken driver
+        return None
 
 
 def capture_snapshot(device_index: int = 0, meminfo_path: Optional[str] = None) -> MemorySnapshot:
-    """Capture host (/proc/meminfo) and device (torch.cuda) counters; works
-    without a GPU."""
-    system = read_system_memory(meminfo_path or "/proc/meminfo")
-    gpu_available = False
-    free = total = allocated = reserved = 0
-    try:
-        import torch
-
-        if torch.cuda.is_available():
-            free, total = (int(v) for v in torch.cuda.mem_get_info(device_index))
-            # One read of the allocator's nested counters (memory_allocated /
-            # memory_reserved each rebuild the flattened statistics dict).
-            stats = torch.cuda.memory_stats_as_nested_dict(device_index)
-            allocated = int(stats.get("allocated_bytes", {}).get("all", {}).get("current", 0))
-            reserved = int(stats.get("reserved_bytes", {}).get("all", {}).get("current", 0))
-            gpu_available = True
-    except Exception:  # pragma: no cover - broken driver / CPU-only host
-        gpu_available = False
+    """Read the host and device counters now (a host without a GPU gives
+    zero device fields and ``gpu_available=False``)."""
+    host = read_system_memory_platform(meminfo_path)
+    device = _device_counters(device_index)
+    free, total, allocated, reserved = device if device is not None else (0, 0, 0, 0)
     return MemorySnapshot(
-        gpu_available=gpu_available,
-        system_total_bytes=system["MemTotal"],
-        system_available_bytes=system["MemAvailable"],
-        system_free_bytes=system["MemFree"],
-        cached_bytes=system["Cached"],
-        swap_total_bytes=system["SwapTotal"],
-        swap_free_bytes=system["SwapFree"],
-        device_free_bytes=free,
-        device_total_bytes=total,
-        device_allocated_bytes=allocated,
-        device_reserved_bytes=reserved,
-    )
+        gpu_available=device is not None,
+        system_total_bytes=host["MemTotal"], system_available_bytes=host["MemAvailable"],
+        system_free_bytes=host["MemFree"], cached_bytes=host["Cached"],
+        swap_total_bytes=host["SwapTotal"], swap_free_bytes=host["SwapFree"],
+        device_free_bytes=free, device_total_bytes=total,
+        device_allocated_bytes=allocated, device_reserved_bytes=reserved)
 
 
 class MemoryPressureError(RuntimeError):
-    """Raised when an allocation would breach the reserve (memory_policy.py:272-291)."""
+    """A scratch request that the policy refused, with the numbers behind
+    the refusal: bytes asked for, bytes admissible, the snapshot and the
+    caller's context label."""
 
     def __init__(self, message: str, need_bytes: int, usable_bytes: int,
                  snapshot: MemorySnapshot, context: str = ""):
@@ -158,14 +193,23 @@ class MemoryPressureError(RuntimeError):
         self.context = context
 
     def as_dict(self) -> dict:
-        return {"error": "MemoryPressureError", "context": self.context,
+        return {"error": type(self).__name__, "context": self.context,
                 "need_bytes": self.need_bytes, "usable_bytes": self.usable_bytes,
                 "message": str(self), "snapshot": self.snapshot.as_dict()}
 
 
+def _non_negative(name: str, value: int) -> None:
+    if value < 0:
+        raise ValueError(f"{name} must be non-negative, got {value}")
+
+
+def _label(kind: str, context: str) -> str:
+    return f"{kind} [{context}]" if context else kind
+
+
 @dataclass(frozen=True)
 class MemoryPolicy:
-    """Admission policy (memory_policy.py:294-421)."""
+    """Reserve-based admission of scratch buffers (see the module docstring)."""
 
     reserve_bytes: int = field(default_factory=default_reserve_bytes)
     safety_slack_bytes: int = DEFAULT_SAFETY_SLACK_BYTES
@@ -173,60 +217,62 @@ class MemoryPolicy:
     reflect_outstanding: bool = field(default_factory=reflect_outstanding_counters)
 
     def usable_bytes(self, snapshot: MemorySnapshot, outstanding_bytes: int = 0) -> int:
-        if outstanding_bytes < 0:
-            raise ValueError(f"outstanding_bytes must be non-negative, got {outstanding_bytes}")
-        pending = 0 if self.reflect_outstanding else outstanding_bytes
-        return max(0, snapshot.binding_available_bytes - self.reserve_bytes - pending)
+        """Bytes that may still be committed without touching the reserve."""
+        _non_negative("outstanding_bytes", outstanding_bytes)
+        counted = 0 if self.reflect_outstanding else outstanding_bytes
+        return max(0, snapshot.binding_available_bytes - self.reserve_bytes - counted)
+
+    def _refusal(self, need: int, usable: int, snapshot: MemorySnapshot,
+                 outstanding: int, context: str) -> Optional[str]:
+        ceiling = self.max_single_alloc_bytes
+        if ceiling is not None and need > ceiling:
+            return (f"{_label('single-allocation ceiling exceeded', context)}: one buffer of "
+                    f"{format_bytes(need)} is above the {format_bytes(ceiling)} ceiling")
+        if need <= usable:
+            return None
+        counted = "" if self.reflect_outstanding or not outstanding else \
+            f" - {format_bytes(outstanding)} outstanding"
+        return (f"{_label('memory-pressure abort', context)}: {format_bytes(need)} requested, "
+                f"{format_bytes(usable)} admissible = "
+                f"{format_bytes(snapshot.binding_available_bytes)} free - "
+                f"{format_bytes(self.reserve_bytes)} reserve{counted}")
 
     def check(self, need_bytes: int, snapshot: MemorySnapshot, outstanding_bytes: int = 0,
               context: str = "") -> int:
-        if need_bytes < 0:
-            raise ValueError(f"need_bytes must be non-negative, got {need_bytes}")
+        """Admit ``need_bytes`` or raise MemoryPressureError; returns the
+        admissible budget the request was measured against."""
+        _non_negative("need_bytes", need_bytes)
         usable = self.usable_bytes(snapshot, outstanding_bytes)
-        if self.max_single_alloc_bytes is not None and need_bytes > self.max_single_alloc_bytes:
-            raise MemoryPressureError(
-                f"single-allocation ceiling exceeded{self._ctx(context)}: need "
-                f"{format_bytes(need_bytes)} > ceiling {format_bytes(self.max_single_alloc_bytes)}",
-                need_bytes, usable, snapshot, context)
-        if need_bytes > usable:
-            detail = (f"; outstanding {format_bytes(outstanding_bytes)} already committed"
-                      if outstanding_bytes else "")
-            raise MemoryPressureError(
-                f"memory-pressure abort{self._ctx(context)}: need {format_bytes(need_bytes)} but "
-                f"only {format_bytes(usable)} usable (binding available "
-                f"{format_bytes(snapshot.binding_available_bytes)}, reserve "
-                f"{format_bytes(self.reserve_bytes)}{detail})",
-                need_bytes, usable, snapshot, context)
+        reason = self._refusal(need_bytes, usable, snapshot, outstanding_bytes, context)
+        if reason is not None:
+            raise MemoryPressureError(reason, need_bytes, usable, snapshot, context)
         return usable
 
     def check_after_commit(self, snapshot: MemorySnapshot,
                            pre_snapshot: Optional[MemorySnapshot] = None,
                            expected_bytes: int = 0, context: str = "post-commit") -> None:
-        """Allocator growth must cover the request; the reserve floor must hold
-        (memory_policy.py:366-408)."""
+        """Confirm a commitment: the caching allocator grew by at least
+        ``expected_bytes`` since ``pre_snapshot`` (when both are given), and
+        free memory is still above the reserve less the slack."""
         if pre_snapshot is not None and expected_bytes > 0:
-            growth = snapshot.device_allocated_bytes - pre_snapshot.device_allocated_bytes
-            if growth < expected_bytes:
+            grew = snapshot.device_allocated_bytes - pre_snapshot.device_allocated_bytes
+            if grew < expected_bytes:
                 raise MemoryPressureError(
-                    f"allocator commitment failure{self._ctx(context)}: expected at least "
-                    f"{format_bytes(expected_bytes)} allocated growth, observed only "
-                    f"{format_bytes(growth)}",
+                    f"{_label('allocator commitment failure', context)}: the allocator grew by "
+                    f"{format_bytes(grew)}, the buffers need {format_bytes(expected_bytes)}",
                     expected_bytes, self.usable_bytes(snapshot), snapshot, context)
         floor = self.reserve_bytes - self.safety_slack_bytes
-        if snapshot.binding_available_bytes < floor:
+        left = snapshot.binding_available_bytes
+        if left < floor:
             raise MemoryPressureError(
-                f"reserve breached{self._ctx(context)}: binding available "
-                f"{format_bytes(snapshot.binding_available_bytes)} < floor {format_bytes(floor)} "
-                f"(reserve {format_bytes(self.reserve_bytes)}, slack "
-                f"{format_bytes(self.safety_slack_bytes)})",
+                f"{_label('reserve breached', context)}: {format_bytes(left)} free after the "
+                f"commitment, below the {format_bytes(self.reserve_bytes)} reserve less "
+                f"{format_bytes(self.safety_slack_bytes)} slack",
                 0, self.usable_bytes(snapshot), snapshot, context)
 
     def describe(self, snapshot: MemorySnapshot) -> dict:
+        """The policy's settings and its budget on ``snapshot``."""
         return {"reserve_bytes": self.reserve_bytes,
                 "safety_slack_bytes": self.safety_slack_bytes,
                 "max_single_alloc_bytes": self.max_single_alloc_bytes,
                 "usable_bytes": self.usable_bytes(snapshot), "snapshot": snapshot.as_dict()}
-
-    @staticmethod
-    def _ctx(context: str) -> str:
-        return f" [{context}]" if context else ""

@@ -26,6 +26,27 @@ extern "C" {
 int exl3_hadamard128(const float* in, float* out, int64_t rows, int64_t cols, int side,
                      void* stream);
 
+/* The two fused steps of regularize (regularize.py:159-173): each divides
+ * the matrix by a scale vector and applies the blockwise Hadamard transform
+ * in one pass over HBM, the arithmetic of a division (correctly rounded
+ * fp32) followed by exl3_hadamard128.
+ * side = 1: out = (in / divisor[col]) @ H, divisor of `cols` floats (the
+ *           fold of sv before H_r); slice_sumsq, if not NULL, receives the
+ *           sum of squares of every 32-element slice of every output row,
+ *           slice_sumsq[row * (cols / 32) + slice] (the first pass of the
+ *           row RMS that regularize takes next).
+ * side = 0: out = H @ (in / divisor[row]), divisor of `rows` floats (the
+ *           fold of su before H_l); slice_sumsq must be NULL.
+ * divisor may be NULL (no division); in == out is allowed. */
+int exl3_hadamard128_scaled(const float* in, float* out, int64_t rows, int64_t cols, int side,
+                            const float* divisor, float* slice_sumsq, void* stream);
+
+/* Second pass of block_rms (regularize.py:41-56) over slice sums made
+ * elsewhere: out[o] = sqrt(S_o / n), S_o the sum of slice_sumsq[o * slices
+ * + s] over s = 0 .. slices - 1 taken in slice order. */
+int exl3_block_rms_from_slices(const float* slice_sumsq, float* out, int64_t outputs, int64_t n,
+                               int64_t slices, void* stream);
+
 /* Replaces block_rms (regularize.py:41-56): out = sqrt(S / n), S the sum of
  * squares along `dim` (0: over rows, one output per column; 1: over
  * columns, one per row) taken in slices of `blocksize` whose sums are

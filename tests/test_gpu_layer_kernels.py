@@ -227,3 +227,75 @@ def test_hessian_from_half_activations_matches_float32(torch_mod):
         scale = np.abs(want).max()
         np.testing.assert_allclose(H.cpu().numpy(), want, rtol=0, atol=1e-5 * scale)
         np.testing.assert_allclose(H32.cpu().numpy(), want, rtol=0, atol=1e-5 * scale)
+
+
+@pytest.mark.parametrize("shape", [(128, 128), (256, 384), (384, 1024)])
+def test_hadamard128_scaled_equals_divide_then_transform(torch_mod, shape):
+    """exl3_hadamard128_scaled (the fused folds of regularize.py:159-173):
+    bit for bit the torch division followed by exl3_hadamard128, on both
+    sides and in place; the row slice sums of squares equal float64 sums
+    of the transformed rows' 32-element slices."""
+    torch = torch_mod
+    from exl3_intel_arc_quantizer_amd import _native, hadamard
+    k, n = shape
+    rng = np.random.default_rng(k + n)
+    x = torch.from_numpy(rng.standard_normal((k, n)).astype(np.float32)).cuda()
+    dcol = torch.from_numpy((rng.random(n) * 3 + 0.1).astype(np.float32)).cuda()
+    drow = torch.from_numpy((rng.random(k) * 3 - 1.6).astype(np.float32)).cuda()
+    out = torch.empty_like(x)
+    sq = torch.empty((k, n // 32), dtype=torch.float32, device="cuda")
+    _native.hadamard128_scaled(x, out, 1, divisor=dcol, slice_sumsq=sq)
+    want = hadamard.preapply_had_r(x / dcol.reshape(1, n))
+    assert torch.equal(out, want)
+    o64 = want.cpu().numpy().astype(np.float64)
+    np.testing.assert_allclose(sq.cpu().numpy(), (o64 ** 2).reshape(k, n // 32, 32).sum(-1),
+                               rtol=2e-6)
+    _native.hadamard128_scaled(x, out, 0, divisor=drow)
+    assert torch.equal(out, hadamard.preapply_had_l(x / drow.reshape(k, 1)))
+    y = x.clone()
+    _native.hadamard128_scaled(y, y, 0, divisor=drow)
+    assert torch.equal(y, out)
+    _native.hadamard128_scaled(x, out, 1)
+    assert torch.equal(out, hadamard.preapply_had_r(x))
+    rms = torch.empty(k, dtype=torch.float32, device="cuda")
+    _native.block_rms_from_slices(sq, rms, n)
+    np.testing.assert_allclose(rms.cpu().numpy(), np.sqrt((o64 ** 2).mean(axis=1)), rtol=2e-6)
+    with pytest.raises(RuntimeError):                           # wrong length for side 0
+        _native.hadamard128_scaled(x, out, 0, divisor=torch.ones(k + 1, device="cuda"))
+    with pytest.raises(RuntimeError):
+        _native.hadamard128_scaled(x, out, 0, slice_sumsq=sq)    # sums only with side 1
+
+
+@pytest.mark.parametrize("name", ["columns", "tiny", "dead", "skew_below", "skew_above"])
+def test_regularize_closed_forms_gpu(torch_mod, name):
+    """The product's regularize (three passes over the fused kernels) gives
+    the scale values the definition fixes (tests/regularize_cases.py), the
+    flag and skew, and decodes back to W."""
+    torch = torch_mod
+    from exl3_intel_arc_quantizer_amd.hadamard import weight_from_quantized
+    from exl3_intel_arc_quantizer_amd.regularize import regularize
+
+    from .regularize_cases import K, N, cases, check
+    case = cases()[name]
+    W = torch.from_numpy(case["W"]).cuda()
+    args = {}
+    res = regularize(W, torch.ones((K, 1), device="cuda"), torch.ones((1, N), device="cuda"),
+                     quant_args=args, H_diag=torch.from_numpy(case["H_diag"]).cuda())
+    assert torch.equal(W, torch.from_numpy(case["W"]).cuda())          # input untouched
+    assert args["zeros"] is False and res.zeros is False
+    if "skew" in case["expected"]:
+        assert res.skew_factor == pytest.approx(case["expected"]["skew"], rel=1e-5)
+    back = weight_from_quantized(res.weight, res.su, res.sv)
+    check(name, case, res.weight.cpu().numpy(), res.su.cpu().numpy(), res.sv.cpu().numpy(),
+          res.apply_out_scales, back.cpu().numpy())
+    if name == "dead":
+        assert res.out_channel_scales[0, 5].item() == pytest.approx(0.1)
+    # Forced flags and the all-zero weight (quant_args["zeros"]).
+    z = regularize(torch.zeros((K, N), device="cuda"), torch.ones((K, 1), device="cuda"),
+                   torch.ones((1, N), device="cuda"), quant_args={"apply_out_scales": False})
+    assert z.zeros and z.apply_out_scales and torch.count_nonzero(z.weight) == 0
+    assert torch.count_nonzero(z.sv) == 0
+    off = regularize(W, torch.ones((K, 1), device="cuda"), torch.ones((1, N), device="cuda"),
+                     quant_args={"apply_out_scales": False},
+                     H_diag=torch.from_numpy(case["H_diag"]).cuda())
+    assert not off.apply_out_scales

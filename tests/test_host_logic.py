@@ -132,3 +132,81 @@ def test_extension_validation_without_gpu():
         ext.quantize_tiles(t, t, t, t, t, 2, False, True)
     with pytest.raises(RuntimeError, match="cb must be"):
         ext.decode_codebook(7, torch.zeros(65536, dtype=torch.float16))
+
+
+def _snap(device_free, system_available=64 * BYTES_PER_GIB, gpu=True, allocated=0):
+    from exl3_intel_arc_quantizer_amd.memory_policy import MemorySnapshot
+    return MemorySnapshot(gpu_available=gpu, system_total_bytes=128 * BYTES_PER_GIB,
+                          system_available_bytes=system_available, system_free_bytes=0,
+                          cached_bytes=0, swap_total_bytes=0, swap_free_bytes=0,
+                          device_free_bytes=device_free if gpu else 0,
+                          device_total_bytes=288 * 10 ** 9 if gpu else 0,
+                          device_allocated_bytes=allocated, device_reserved_bytes=0)
+
+
+def test_policy_binds_on_free_hbm():
+    """memory_policy.py:194-421 with the discrete-HBM binding figure: free
+    device memory on a GPU host (host RAM is a separate pool and does not
+    bind, even when smaller), host available memory without a GPU."""
+    assert _snap(200 * BYTES_PER_GIB, system_available=3 * BYTES_PER_GIB) \
+        .binding_available_bytes == 200 * BYTES_PER_GIB
+    assert _snap(0, system_available=10 * BYTES_PER_GIB, gpu=False) \
+        .binding_available_bytes == 10 * BYTES_PER_GIB
+    d = _snap(5).as_dict()
+    assert d["binding_available_bytes"] == 5 and d["device_total_bytes"] == 288 * 10 ** 9
+
+
+def test_policy_admission_boundary_and_outstanding():
+    pol = MemoryPolicy(reserve_bytes=6 * BYTES_PER_GIB, reflect_outstanding=True)
+    snap = _snap(10 * BYTES_PER_GIB)
+    assert pol.usable_bytes(snap) == 4 * BYTES_PER_GIB
+    assert pol.usable_bytes(_snap(3 * BYTES_PER_GIB)) == 0
+    assert pol.check(4 * BYTES_PER_GIB, snap) == 4 * BYTES_PER_GIB      # exactly the budget
+    with pytest.raises(MemoryPressureError) as ei:
+        pol.check(4 * BYTES_PER_GIB + 1, snap, context="K=2 B=8")
+    err = ei.value
+    assert err.need_bytes == 4 * BYTES_PER_GIB + 1 and err.usable_bytes == 4 * BYTES_PER_GIB
+    assert "memory-pressure abort [K=2 B=8]" in str(err) and "reserve" in str(err)
+    assert err.as_dict()["context"] == "K=2 B=8"
+    # The free-HBM counter already reflects live allocations by default;
+    # with reflect_outstanding off they are subtracted and named.
+    assert pol.usable_bytes(snap, outstanding_bytes=BYTES_PER_GIB) == 4 * BYTES_PER_GIB
+    strict = MemoryPolicy(reserve_bytes=6 * BYTES_PER_GIB, reflect_outstanding=False)
+    assert strict.usable_bytes(snap, outstanding_bytes=BYTES_PER_GIB) == 3 * BYTES_PER_GIB
+    with pytest.raises(MemoryPressureError, match="1.00 GiB outstanding"):
+        strict.check(3 * BYTES_PER_GIB + 1, snap, outstanding_bytes=BYTES_PER_GIB)
+    with pytest.raises(ValueError):
+        pol.check(-1, snap)
+
+
+def test_policy_ceiling_and_post_commit():
+    from exl3_intel_arc_quantizer_amd.memory_policy import BYTES_PER_MIB, format_bytes
+    pol = MemoryPolicy(reserve_bytes=0, max_single_alloc_bytes=4 * BYTES_PER_GIB)
+    snap = _snap(30 * BYTES_PER_GIB)
+    pol.check(4 * BYTES_PER_GIB, snap)
+    with pytest.raises(MemoryPressureError, match="single-allocation ceiling"):
+        pol.check(4 * BYTES_PER_GIB + 1, snap)
+    post = MemoryPolicy(reserve_bytes=6 * BYTES_PER_GIB, safety_slack_bytes=256 * BYTES_PER_MIB)
+    post.check_after_commit(_snap(6 * BYTES_PER_GIB - 200 * BYTES_PER_MIB))   # within slack
+    with pytest.raises(MemoryPressureError, match="reserve breached"):
+        post.check_after_commit(_snap(6 * BYTES_PER_GIB - 300 * BYTES_PER_MIB))
+    before, after = _snap(100 * BYTES_PER_GIB), _snap(99 * BYTES_PER_GIB, allocated=BYTES_PER_GIB)
+    post.check_after_commit(after, pre_snapshot=before, expected_bytes=BYTES_PER_GIB)
+    with pytest.raises(MemoryPressureError, match="allocator commitment failure"):
+        post.check_after_commit(after, pre_snapshot=before, expected_bytes=BYTES_PER_GIB + 1)
+    assert format_bytes(None) == "n/a" and format_bytes(512) == "512 B"
+    assert format_bytes(3 * BYTES_PER_MIB // 2) == "1.5 MiB"
+    assert format_bytes(-5 * BYTES_PER_GIB // 2) == "-2.50 GiB"
+    assert post.describe(snap)["usable_bytes"] == 24 * BYTES_PER_GIB
+
+
+def test_platform_memory_source(tmp_path):
+    from exl3_intel_arc_quantizer_amd.memory_policy import (read_system_memory_platform,
+                                                            read_system_memory_windows)
+    live = read_system_memory_platform()
+    assert live["MemTotal"] > 0 and live["MemAvailable"] <= live["MemTotal"]
+    p = tmp_path / "m"
+    p.write_text("MemTotal:       32 kB\nMemAvailable:   16 kB\n")
+    assert read_system_memory_platform(str(p))["MemTotal"] == 32 * 1024
+    with pytest.raises(OSError):
+        read_system_memory_windows()

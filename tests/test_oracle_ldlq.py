@@ -54,6 +54,19 @@ def test_regularize_round_trip_and_scales():
     assert apply_out is True
 
 
+@pytest.mark.parametrize("name", ["columns", "tiny", "dead", "skew_below", "skew_above"])
+def test_regularize_closed_forms(name):
+    """regularize.py:83-211: scale values fixed by the definition (see
+    tests/regularize_cases.py): su = RMS / -1.24371088 + 1e-10 with the sign,
+    constant and 1e-10 placement pinned, sv = column RMS / mean RMS, zero
+    rows and columns, the 0.15 skew cutoff over the top 2 % of the diagonal."""
+    from .regularize_cases import cases, check
+    case = cases()[name]
+    reg_w, su, sv, apply_out = ldlq_ref.regularize(case["W"], case["H_diag"])
+    back = ldlq_ref.weight_from_quantized(reg_w, su, sv)
+    check(name, case, reg_w, su, sv, apply_out, back)
+
+
 def test_block_ldl_factor_and_fold():
     """ldlq.py:76-142: L L^T = H; transformed = L with each column block
     times the inverse of its diagonal block, diagonal blocks identity."""
