@@ -34,6 +34,8 @@ _SIGNATURES = {
     "exl3_backpointer_slot": (_c_i64, [_c_int, _c_i64]),
     "exl3_quantize_tiles": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int,
                                      _c_int, _c_int, _c_int, _c_i64, _c_vp]),
+    "exl3_quantize_tiles_noalloc": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
+                                             _c_int, _c_vp]),
     "exl3_forward_pass": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
                                    _c_int, _c_int, _c_int, _c_vp]),
     "exl3_backward_pass": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_int,

@@ -51,6 +51,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "../../include/exl3_encoder.h"
@@ -1315,6 +1316,44 @@ __global__ void probe_hfma_kernel(const uint16_t* __restrict__ a, const uint16_t
 
 static hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// ------------------------------------------- scratch of the no-alloc entry
+
+// temp_costs then temp_edges of exl3_quantize_tiles_noalloc's tiles. Every
+// GPU the library runs on holds its own copy from module load until the
+// process ends. Host code never uses this name as an address: it is a
+// host-side stand-in, and kernels get the device address that
+// hipGetSymbolAddress returns for the current GPU.
+__device__ __align__(256) uint8_t scratch[EXL3_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of `scratch` on the calling thread's current GPU, looked
+// up once per device with that device current.
+static int noalloc_scratch(uint8_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error("quantize_tiles_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return set_error("quantize_tiles_noalloc: device %d outside 0..%d", dev,
+                     kMaxScratchDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error("quantize_tiles_noalloc: hipGetSymbolAddress(scratch) failed on device "
+                       "%d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+static int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
+
 static int validate_common(int K, int cb, int L) {
   if (K < 1 || K > 8) return set_error("K must be in 1..8, got %d", K);
   if (cb < 0 || cb > 2) return set_error("cb must be 0, 1, or 2, got %d", cb);
@@ -1582,6 +1621,30 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
     if (launch_traceback(t2, st)) return 1;
   }
   return 0;
+}
+
+int exl3_quantize_tiles_noalloc(const float* in, float* out_w, int16_t* out_idx, int64_t n,
+                                int K, int cb, int L, int generic, void* stream) {
+  if (validate_common(K, cb, L)) return 1;
+  if (n <= 0) return set_error("num_tiles must be positive, got %lld", (long long)n);
+  if (!in || !out_w || !out_idx) return set_error("NULL buffer");
+  // Per tile: 2 x E fp16 terminal costs and one tile block of temp_edges.
+  const int64_t costs_per_tile = 4 * (int64_t)(65536 >> K);
+  const int64_t edges_per_tile = (int64_t)exl3::tile_scratch_bytes(layout_for(K), L);
+  const int64_t limit = EXL3_NOALLOC_SCRATCH_BYTES;
+  const int64_t max_tiles = (limit - 255) / (costs_per_tile + edges_per_tile);
+  if (n > max_tiles)
+    return set_error("quantize_tiles_noalloc: %lld tiles exceed the %lld-byte static scratch, "
+                     "which holds at most %lld tiles at K=%d, L=%d; split the batch",
+                     (long long)n, (long long)limit, (long long)max_tiles, K, L);
+  uint8_t* base = nullptr;
+  if (noalloc_scratch(&base)) return 1;
+  uint16_t* temp_costs = reinterpret_cast<uint16_t*>(base);
+  uint8_t* temp_edges = base + align256(n * costs_per_tile);
+  // Every scratch byte a kernel reads was written earlier in the same call,
+  // so nothing is cleared.
+  return exl3_quantize_tiles(in, out_w, out_idx, temp_costs, temp_edges, n, n, K, cb, L, generic,
+                             0, stream);
 }
 
 int exl3_prepare_tiles(const float* raw, float* out, int64_t n, int L, int permute,

@@ -86,6 +86,26 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
                         uint8_t* temp_edges, int64_t batch_cap, int64_t n, int K, int cb, int L,
                         int generic, int64_t wave_cap, void* stream);
 
+/* Bytes of the library's static scratch for exl3_quantize_tiles_noalloc. */
+#define EXL3_NOALLOC_SCRATCH_BYTES ((int64_t)512 << 20)
+
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): exl3_quantize_tiles for n tiles with its temp_costs and
+ * temp_edges in a static device array of EXL3_NOALLOC_SCRATCH_BYTES (512
+ * MiB) that each GPU holds from library load until the process ends. No
+ * hipMalloc, hipFree or allocating library call is made. Limit: all n tiles
+ * must fit at once, n <= floor((EXL3_NOALLOC_SCRATCH_BYTES - 255) /
+ * (4 (65536 >> K) + exl3_scratch_edges_bytes(K, L, 1))), e.g. 244 tiles at
+ * K = 2 and 500 at K = 4 (L = 256); larger n is rejected with an error and
+ * nothing is launched. Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (on different streams, or from several threads
+ * without ordering) race and corrupt each other's results. Results equal
+ * exl3_quantize_tiles'. in / out_w / out_idx as there; the device is the
+ * one current on the calling thread, which must be `stream`'s. */
+int exl3_quantize_tiles_noalloc(const float* in, float* out_w, int16_t* out_idx, int64_t n,
+                                int K, int cb, int L, int generic, void* stream);
+
 /* Replaces quantize_tiles_forward_pass (quantize_xpu.cpp:169-215,
  * quantize_kernels.sycl:658-704): one forward add-compare-select pass over
  * the ring with rotation `roll`; tile t is constrained to start from edge
