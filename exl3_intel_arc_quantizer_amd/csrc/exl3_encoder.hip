@@ -79,20 +79,33 @@ __device__ __forceinline__ f16 f16_bits(uint32_t b) {
 }
 __device__ __forceinline__ uint16_t bits_f16(f16 h) { return __builtin_bit_cast(uint16_t, h); }
 
-// fp16 value of state s (reference trellis_format.py:41-81,
-// quantize_kernels.sycl:51-73; upstream codebook.cuh:56-123).
-__device__ __forceinline__ f16 decode_state(int cb, uint32_t s) {
+// The codebooks (reference trellis_format.py:41-81, quantize_kernels.sycl:51-73;
+// upstream codebook.cuh:56-123) hash state s to x = s * M (+ A for 3INST)
+// modulo 2^32 and decode x. The hash is affine in s, so for s = s1 + s2
+// (disjoint bit fields) x = hash(s1) + s2 * M: the traceback trees compute
+// one product per lane and add compile-time offsets for the other fields,
+// instead of a quarter-rate v_mul_lo_u32 per leaf.
+__host__ __device__ constexpr uint32_t hash_mult(int cb) {
+  return cb == 2 ? 0x83DCD12Du : (cb == 0 ? 89226354u : 0xCBAC1FEDu);
+}
+__device__ __forceinline__ uint32_t hash_state(int cb, uint32_t s) {
+  return s * hash_mult(cb) + (cb == 0 ? 64248484u : 0u);
+}
+__device__ __forceinline__ f16 decode_hash(int cb, uint32_t x) {
   if (cb == 2) {
-    const uint32_t x = s * 0x83DCD12Du;
     // v_sad_u8(x, 0, 0x6400) = 0x6400 + the sum of x's four bytes (each
     // |byte - 0|) in one instruction; 0x6400 + bsum is the fp16 encoding of
     // 1024 + bsum (bsum <= 1020). One fused fp16 FMA.
     const uint32_t h = __builtin_amdgcn_sad_u8(x, 0u, 0x6400u);
     return __builtin_fmaf16(f16_bits(h), f16_bits(0x1EEEu), f16_bits(0xC931u));
   }
-  uint32_t x = (cb == 0) ? (s * 89226354u + 64248484u) : (s * 0xCBAC1FEDu);
   x = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
   return f16_bits(x & 0xFFFFu) + f16_bits(x >> 16);
+}
+
+// fp16 value of state s.
+__device__ __forceinline__ f16 decode_state(int cb, uint32_t s) {
+  return decode_hash(cb, hash_state(cb, s));
 }
 
 __global__ void decode_codebook_kernel(int cb, uint16_t* __restrict__ out) {
@@ -723,11 +736,54 @@ __device__ __forceinline__ uint32_t row_pos(uint32_t x) {
   return exl3::cost_row_pos(K, x);
 }
 
+// The states a traceback tree decodes, split into the part that depends on
+// the lane (and the walk's edge) and the part that depends on the register
+// index r. Leaf n = (lane << RLOG | r) & (2^(K(D+1)) - 1); every bit of the
+// state at level m is a copy of one bit of n or of the edge, so the state is
+// the disjoint OR (= sum) of its value with r = 0 and its value with lane = 0
+// and edge = 0. hash_state is affine, so the hash of the leaf's state is the
+// lane's hash (one multiply per level) plus a compile-time offset per r.
+template <int K, int D, int RLOG>
+struct TreeFields {
+  static constexpr int NB = 1 << K, KR = 16 - K, KS = 16 - 2 * K;
+  static constexpr int NLOG = K * (D + 1);
+  static constexpr uint32_t NMASK = (1u << NLOG) - 1u;
+  uint32_t nl, h0;
+
+  __device__ __forceinline__ TreeFields(int lane, uint32_t edge_hi)
+      : nl(((uint32_t)lane << RLOG) & NMASK), h0(edge_hi) {}
+
+  // x_m of leaf n (the predecessor edge at level m) with edge part hh.
+  __host__ __device__ static constexpr uint32_t x_at(uint32_t n, uint32_t hh, int m) {
+    uint32_t x = ((n >> (K * D)) << KS) | hh;
+    for (int j = 1; j <= m; ++j) x = (((n >> (K * (D - j))) & (NB - 1)) << KS) | (x >> K);
+    return x;
+  }
+  // State decoded at level m (digit k_{m+1} over x_m).
+  __host__ __device__ static constexpr uint32_t level_state(uint32_t n, uint32_t hh, int m) {
+    const int lo = K * (D - 1 - m);
+    return (((n >> lo) & (NB - 1)) << KR) | x_at(n, hh, m);
+  }
+  __device__ __forceinline__ uint32_t level_hash(int cb, int m) const {
+    return hash_state(cb, level_state(nl, h0, m));
+  }
+  __host__ __device__ static constexpr uint32_t level_offset(int cb, int m, int r) {
+    return level_state((uint32_t)r & NMASK, 0u, m) * hash_mult(cb);
+  }
+  // State decoded at the top (digit k_0 over the walk's edge).
+  __device__ __forceinline__ uint32_t top_hash(int cb, uint32_t edge) const {
+    return hash_state(cb, ((nl >> (K * D)) << KR) | edge);
+  }
+  __host__ __device__ static constexpr uint32_t top_offset(int cb, int r) {
+    return ((((uint32_t)r & NMASK) >> (K * D)) << KR) * hash_mult(cb);
+  }
+};
+
 template <int K, int CB, int D, bool INIT>
 __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ leaf, uint32_t edge,
                                               const uint16_t* __restrict__ wbits, int ri, int L,
                                               int lane, int pre) {
-  constexpr int NB = 1 << K, KR = 16 - K, KS = 16 - 2 * K;
+  constexpr int NB = 1 << K, KS = 16 - 2 * K;
   constexpr int NLOG = K * (D + 1);
   constexpr int RLOG = NLOG > 6 ? NLOG - 6 : 0;
   constexpr int R = 1 << RLOG;
@@ -738,6 +794,7 @@ __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ leaf,
   uint32_t nid[R];
   uint32_t xs[R][D + 1];
   uint32_t v[R];
+  TreeFields<K, D, RLOG> tf(lane, h0);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const uint32_t n = (((uint32_t)lane << RLOG) | (uint32_t)r) & NMASK;
@@ -771,10 +828,10 @@ __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ leaf,
     if (rm < 0) rm += L;
     const f16 wm = f16_bits(wbits[rm]);
     const int nr = lo < RLOG ? R : 1;  // registers still distinct
+    const uint32_t hl = tf.level_hash(CB, m);
 #pragma unroll
     for (int r = 0; r < nr; ++r) {
-      const uint32_t k = (nid[r] >> lo) & (NB - 1);
-      const f16 dh = decode_state(CB, (k << KR) | xs[r][m]) - wm;
+      const f16 dh = decode_hash(CB, hl + TreeFields<K, D, RLOG>::level_offset(CB, m, r)) - wm;
       v[r] = bits_f16(__builtin_fmaf16(dh, dh, f16_bits(v[r])));
     }
 #pragma unroll
@@ -798,11 +855,12 @@ __device__ __forceinline__ uint32_t tb_branch(const uint16_t* __restrict__ leaf,
   // Step i: key minimum over k_0, bits [K D, NLOG) of n.
   const f16 w = f16_bits(wbits[ri]);
   const int nr = (K * D) < RLOG ? R : 1;
+  const uint32_t ht = tf.top_hash(CB, edge);
   uint32_t key = 0xFFFFFFFFu;
 #pragma unroll
   for (int r = 0; r < nr; ++r) {
     const uint32_t k0 = nid[r] >> (K * D);
-    const f16 dh = decode_state(CB, (k0 << KR) | edge) - w;
+    const f16 dh = decode_hash(CB, ht + TreeFields<K, D, RLOG>::top_offset(CB, r)) - w;
     const f16 err = __builtin_fmaf16(dh, dh, f16_bits(v[r]));
     key = umin(key, ((uint32_t)bits_f16(err) << 16) | k0);
   }
@@ -830,7 +888,7 @@ template <int K, int CB, int D>
 __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, uint32_t edge,
                                             const uint16_t* __restrict__ wbits, int ri, int L,
                                             int lane) {
-  constexpr int NB = 1 << K, KR = 16 - K, KS = 16 - 2 * K;
+  constexpr int NB = 1 << K, KS = 16 - 2 * K;
   constexpr int NLOG = K * (D + 1);
   constexpr int RLOG = NLOG > 6 ? NLOG - 6 : 0;
   constexpr int R = 1 << RLOG;
@@ -841,6 +899,7 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, ui
   uint32_t nid[R];
   uint32_t xs[R][D + 1];
   uint32_t v[R];
+  TreeFields<K, D, RLOG> tf(lane, h0);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const uint32_t n = (((uint32_t)lane << RLOG) | (uint32_t)r) & NMASK;
@@ -860,6 +919,12 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, ui
 #pragma unroll
     for (int u = 0; u < CH; ++u) v[c * CH + u] = q[u];
   }
+  // Every load of the tree is issued before any of it is used: a 32-byte
+  // tree (K = 5) is two dwordx4 loads, which the scheduler otherwise put on
+  // one register quad, one round trip after the other (pass-2 traceback at
+  // 4096 tiles 256 -> 211 us). Smaller trees are one load and keep the
+  // scheduler's freedom.
+  if constexpr (R * 2 > 16) __builtin_amdgcn_sched_barrier(0);
 
   uint32_t lvl[D > 0 ? D : 1][R];
 #pragma unroll
@@ -869,10 +934,11 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, ui
     if (rm < 0) rm += L;
     const f16 wm = f16_bits(wbits[rm]);
     const int nr = lo < RLOG ? R : 1;  // registers still distinct
+    const uint32_t hl = tf.level_hash(CB, m);
 #pragma unroll
     for (int r = 0; r < nr; ++r) {
       const uint32_t k = (nid[r] >> lo) & (NB - 1);
-      const f16 dh = decode_state(CB, (k << KR) | xs[r][m]) - wm;
+      const f16 dh = decode_hash(CB, hl + TreeFields<K, D, RLOG>::level_offset(CB, m, r)) - wm;
       v[r] = ((uint32_t)bits_f16(__builtin_fmaf16(dh, dh, f16_bits(v[r]))) << 16) | k;
     }
     if (nr == 1) {
@@ -905,11 +971,12 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, ui
   // Step i: key minimum over k_0, bits [K D, NLOG) of n.
   const f16 w = f16_bits(wbits[ri]);
   const int nr = (K * D) < RLOG ? R : 1;
+  const uint32_t ht = tf.top_hash(CB, edge);
   uint32_t key = 0xFFFFFFFFu;
 #pragma unroll
   for (int r = 0; r < nr; ++r) {
     const uint32_t k0 = nid[r] >> (K * D);
-    const f16 dh = decode_state(CB, (k0 << KR) | edge) - w;
+    const f16 dh = decode_hash(CB, ht + TreeFields<K, D, RLOG>::top_offset(CB, r)) - w;
     const f16 err = __builtin_fmaf16(dh, dh, f16_bits(v[r]));
     key = umin(key, ((uint32_t)bits_f16(err) << 16) | k0);
   }
