@@ -53,6 +53,7 @@ counters (copy-kernel calibration), null when the summary has no row.
 
     python bench.py [--steps 10] [--warmup 2] [--headline-only] [--no-cpu-baseline]
     python bench.py --profile-forward --k-list 4,2   # forward launches only
+    python bench.py --profile-forward --k-list 4 --profile-tiles 256   # one LDLQ call's size
     python bench.py --profile-sweep                   # configs[2] launches only
 """
 
@@ -524,6 +525,9 @@ def main() -> int:
     ap.add_argument("--profile-forward", action="store_true",
                     help="only the configs[1] forward launches the roofline is measured on "
                          "(eight warm-up and four timed per K), for rocprofv3 runs")
+    ap.add_argument("--profile-tiles", type=int, default=0,
+                    help="with --profile-forward: the first N tiles of configs[1] only (256 is "
+                         "the size of each configs[3] LDLQ call)")
     ap.add_argument("--profile-sweep", action="store_true",
                     help="only the configs[2] forward launches (8192 tiles, K=2..6)")
     ap.add_argument("--layer", action="store_true",
@@ -589,8 +593,9 @@ def main() -> int:
 
     if profiling:
         if args.profile_forward:
+            sel = tiles[:args.profile_tiles] if args.profile_tiles > 0 else tiles
             for K in k_list:
-                b = DeviceBatch(tiles, K, torch, ext)
+                b = DeviceBatch(sel, K, torch, ext)
                 for _ in range(8):                   # clocks up, as after the timed steps
                     b.forward_only(b.n)
                 launch_s, n = time_forward(b, torch)
