@@ -217,7 +217,7 @@ class QuantizeExtension:
                 or temp_edges.size(2) != rb):
             raise RuntimeError(
                 f"temp_edges must have shape (B, {rows}, {rb}) for K={K}, L={L} "
-                "(cost-row / backpointer scratch layout)")
+                "(cost-row scratch layout)")
         return batch_cap
 
     # quantize_xpu.cpp:112-167

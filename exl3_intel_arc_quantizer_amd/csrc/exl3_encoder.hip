@@ -5,7 +5,7 @@
 // and its SYCL kernel FusedQuantizeKernel (quantize_kernels.sycl:245-360),
 // re-designed for CDNA4:
 //
-//   acs_forward_rows   K = 1..7. One 1024-thread workgroup per tile, fp16 path
+//   acs_forward_rows   K = 1..8. One 1024-thread workgroup per tile, fp16 path
 //                      costs ping-pong in LDS, each thread owns 64 (edge,
 //                      branch) candidates whose codebook values stay in 32
 //                      VGPRs. A step is a packed subtract and FMA per
@@ -17,16 +17,15 @@
 //                      the path.
 //   acs_forward_generic reference-structured kernel (one edge per thread
 //                      iteration, codebook decoded per candidate, strict fp16
-//                      '<' scan): K = 8 and the force_global_costs variant;
-//                      writes the same scratch layout as the fast kernels.
+//                      '<' scan): the force_global_costs variant; writes the
+//                      same scratch layout as the fast kernels.
 //   traceback_rows_kernel one 64-lane workgroup per tile walks the ring
 //                      backwards; one evaluation of each stored row's tree
 //                      (rebuilding the costs of the unstored steps) yields
 //                      the branches of every step that reads that row.
 //   traceback_stream_kernel the same walk for small batches, with every
 //                      stored row prefetched whole into an LDS ring by
-//                      loader waves; traceback_bp_kernel (K = 8) reads one
-//                      backpointer byte per step.
+//                      loader waves.
 //   finalize_kernel    packing, path cost, distortion, un-permutation;
 //   unpack_kernel      the inverse of the packing (stored-tensor read-back).
 //
@@ -58,7 +57,7 @@
 #include "exl3_errors.h"
 #include "exl3_layout.h"
 
-using exl3::BpLayout;
+using exl3::RowLayout;
 
 typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -163,8 +162,7 @@ __device__ uint32_t block_argmin(const uint16_t* cost, int E, uint32_t* s_red) {
 struct FwdArgs {
   const float* in;
   int n, L, roll, cb;
-  int store_rows;             // backpointer mode: ring rows ri < store_rows are stored
-  int store_from;             // cost-row mode: step rows i in [store_from, L-2] are stored
+  int store_from;             // step rows i in [store_from, L-2] are stored
   const int32_t* pre_states;  // may be NULL: unconstrained
   int64_t pre_stride;         // in int32 elements
   uint8_t* scratch;           // per-tile blocks of (L+1) rows
@@ -228,7 +226,7 @@ __device__ __forceinline__ void forward_epilogue(const FwdArgs& a, int E, const 
 template <int NT, int KS = 0, int PAD = 0>
 __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const uint16_t* src,
                                                int step) {
-  const BpLayout lay = exl3::make_layout(K);
+  const RowLayout lay = exl3::make_layout(K);
   const int E = 65536 >> K;
   const int chunks = E / 8;
   uint4* dst = reinterpret_cast<uint4*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
@@ -264,7 +262,7 @@ struct RowGather {
 
   __device__ __forceinline__ static void store(const FwdArgs& a, const uint16_t* src, int step) {
     constexpr int ks = 16 - 2 * K;
-    const BpLayout lay = exl3::make_layout(K);
+    const RowLayout lay = exl3::make_layout(K);
     vec* dst = reinterpret_cast<vec*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
                                       (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
     if constexpr (exl3::cost_row_tree_bits(K) > 0 && PAD == 0 && W == 8) {
@@ -368,7 +366,7 @@ template <int K>
 struct FastShape {
   static constexpr int G = (K == 1) ? 16 : (K == 2 ? 4 : 1);
   static constexpr int J = (K == 1) ? 2 : (K == 2 ? 4 : (K == 3 ? 8 : (K == 4 ? 4 : 2)));
-  static constexpr int P = (K == 6) ? 2 : (K == 7 ? 4 : 1);
+  static constexpr int P = (K == 6) ? 2 : (K == 7 ? 4 : (K == 8 ? 8 : 1));
 };
 
 template <int K, int G, int J, int P>
@@ -384,13 +382,13 @@ struct FastCfg {
   static_assert(NT == 1024, "fast configurations use 1024 threads");
   static_assert(J % 2 == 0, "edges are processed in packed pairs (j, j + 1)");
   static_assert(G == 1 || G % 2 == 0, "groups are read in 32-bit pairs");
-  static_assert(P == 1 || P == 2 || P == 4, "branch split within a quad");
+  static_assert(P == 1 || P == 2 || P == 4 || P == 8, "branch split within a half row");
 };
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 template <int P>
-__device__ __forceinline__ u16x2 quad_min_u16x2(u16x2 v) {
+__device__ __forceinline__ u16x2 group_min_u16x2(u16x2 v) {
   if (P >= 2) {
     const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(
         0, (int)__builtin_bit_cast(uint32_t, v), 0xB1, 0xF, 0xF, false);
@@ -401,13 +399,20 @@ __device__ __forceinline__ u16x2 quad_min_u16x2(u16x2 v) {
         0, (int)__builtin_bit_cast(uint32_t, v), 0x4E, 0xF, 0xF, false);
     v = __builtin_elementwise_min(v, __builtin_bit_cast(u16x2, o));
   }
+  if (P >= 8) {
+    // Each quad now holds its minimum; row_half_mirror pairs lane i with
+    // lane 7 - i of its half row, which lies in the other quad.
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(
+        0, (int)__builtin_bit_cast(uint32_t, v), 0x141, 0xF, 0xF, false);
+    v = __builtin_elementwise_min(v, __builtin_bit_cast(u16x2, o));
+  }
   return v;
 }
 
 // Cost-row forward pass (K = 1..7): minimum cost per edge, rows to HBM.
 // Thread `unit` owns edges jj*J .. jj*J + J - 1 of G groups (one group, or
 // NV runs of GV consecutive groups when G > 1), in packed pairs (j, j + 1), and the Q = 2^K / P branches k = q*P + p of
-// lane p of its P-lane quad (interleaved, so the quad's LDS reads fall in
+// lane p of its P-lane group (interleaved, so the group's LDS reads fall in
 // different banks). All edges of a group share the 2^K predecessor costs, so
 // each cost is broadcast to both halves of the FMA addend (op_sel) from a
 // 16-bit LDS read (G = 1) or one half of a 32-bit read holding two groups'
@@ -423,8 +428,10 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
   using C = FastCfg<K, G, J, P>;
   constexpr int JP = J / 2;
   constexpr int KS = 16 - 2 * K;
-  constexpr int PAD = K >= 6 ? 2 : 0;               // one dword per branch block (measured
-                                                    // a loss at K <= 5)
+  // One dword per branch block at K = 6, 7 (measured a loss at K <= 5). At
+  // K = 8 a block is one edge, and padding would split the pairs (e, e + 1)
+  // the outputs are stored as; its reads are conflict-free without it.
+  constexpr int PAD = (K == 6 || K == 7) ? 2 : 0;
   constexpr int SP = C::S + PAD;                    // padded block stride
   constexpr int EP = C::E + (1 << K) * PAD;         // padded vector length
   static_assert(C::Q % 2 == 0, "branches are folded two at a time");
@@ -521,7 +528,7 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int jp = 0; jp < JP; ++jp) {
-        const u16x2 v = quad_min_u16x2<P>(__builtin_bit_cast(u16x2, m[g][jp]));
+        const u16x2 v = group_min_u16x2<P>(__builtin_bit_cast(u16x2, m[g][jp]));
         const int e = (grp(g) << K) | (jj * J + 2 * jp);
         if (P == 1 || p == 0) cout[lds_pos<KS, PAD>(e) >> 1] = __builtin_bit_cast(uint32_t, v);
       }
@@ -540,75 +547,40 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
 // --------------------------------------------------------- generic kernel
 
 constexpr int GEN_NT = 256;
-constexpr int GEN_ROW_WORDS = 64;  // the K = 8 backpointer row: 256 bytes
 
 // Reference-structured forward pass for any K (reference_encoder.py:130-204,
 // quantize_kernels.sycl:83-157): per edge, scan branches k = 0..2^K-1 with a
-// strict fp16 '<'; codebook decoded per candidate. It writes the scratch
-// layout of K: cost rows, or (K = 8) backpointer rows assembled in LDS
-// (double-buffered, copied out one step later).
+// strict fp16 '<'; codebook decoded per candidate. It writes the cost rows
+// of the fast kernels' scratch layout.
 __global__ void __launch_bounds__(GEN_NT) acs_forward_generic(FwdArgs a, int K) {
   __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][32768];
-  __shared__ uint32_t s_row[2][GEN_ROW_WORDS];
   __shared__ f16 s_w[256];
   __shared__ uint32_t s_red[GEN_NT / 64];
 
   const int L = a.L;
   const int E = 65536 >> K, KR = 16 - K, NB = 1 << K;
-  const BpLayout lay = exl3::make_layout(K);
-  const bool rows = lay.mode == exl3::MODE_COST_ROWS;
-  const int row_words = lay.row_bytes / 4;
   int pre;
-  forward_prologue<GEN_NT>(a, E, rows, s_w, s_cost[0], pre);
-  for (int w = threadIdx.x; w < 2 * GEN_ROW_WORDS; w += GEN_NT) (&s_row[0][0])[w] = 0;
+  forward_prologue<GEN_NT>(a, E, true, s_w, s_cost[0], pre);
   __syncthreads();
-  uint8_t* tile_bp = a.scratch + (int64_t)blockIdx.x * a.tile_stride;
-  int prev_ri = -1;
 
   for (int i = 0; i < L; ++i) {
     int ri = i + a.roll;
     if (ri >= L) ri -= L;
     const uint16_t* cin = s_cost[i & 1];
     uint16_t* cout = s_cost[(i & 1) ^ 1];
-    uint32_t* row = s_row[i & 1];
-    uint32_t* done = s_row[(i & 1) ^ 1];
-    if (rows) {
-      if (stores_row(a, K, i)) store_cost_row<GEN_NT>(a, K, cin, i - 1);
-    } else if (prev_ri >= 0) {
-      // Flush the previous step's backpointer row (complete since the last
-      // barrier) and clear it for the step after this one.
-      uint32_t* dst = reinterpret_cast<uint32_t*>(tile_bp + (int64_t)prev_ri * lay.row_bytes);
-      for (int w = threadIdx.x; w < row_words; w += GEN_NT) {
-        if (prev_ri < a.store_rows) dst[w] = done[w];
-        done[w] = 0;
-      }
-    }
+    if (stores_row(a, K, i)) store_cost_row<GEN_NT>(a, K, cin, i - 1);
     const f16 w = s_w[ri];
     for (int e = threadIdx.x; e < E; e += GEN_NT) {
       f16 best = 0;
-      int best_k = 0;
       for (int k = 0; k < NB; ++k) {
         const uint32_t sigma = ((uint32_t)k << KR) | (uint32_t)e;
         const f16 dh = decode_state(a.cb, sigma) - w;
         const f16 err = __builtin_fmaf16(dh, dh, f16_bits(cin[sigma >> K]));
-        if (k == 0 || err < best) {
-          best = err;
-          best_k = k;
-        }
+        if (k == 0 || err < best) best = err;
       }
       cout[e] = bits_f16(best);
-      if (!rows && best_k) {
-        const uint32_t bit = exl3::bp_slot(lay, (uint32_t)e) * (uint32_t)lay.BPB;
-        atomicOr(&row[bit >> 5], (uint32_t)best_k << (bit & 31u));
-      }
     }
-    prev_ri = ri;
     __syncthreads();
-  }
-  if (!rows && prev_ri < a.store_rows) {
-    const uint32_t* last = s_row[(L - 1) & 1];
-    uint32_t* dst = reinterpret_cast<uint32_t*>(tile_bp + (int64_t)prev_ri * lay.row_bytes);
-    for (int w = threadIdx.x; w < row_words; w += GEN_NT) dst[w] = last[w];
   }
   forward_epilogue<GEN_NT>(a, E, s_cost[L & 1], s_red);
 }
@@ -626,17 +598,10 @@ __global__ void __launch_bounds__(256) argmin_costs_kernel(const uint16_t* __res
 
 // -------------------------------------------------------------- traceback
 
-__device__ __forceinline__ uint32_t read_backpointer(const uint8_t* row, const BpLayout& l,
-                                                     uint32_t edge) {
-  const uint32_t bit = exl3::bp_slot(l, edge) * (uint32_t)l.BPB;
-  const uint32_t word = reinterpret_cast<const uint32_t*>(row)[bit >> 5];
-  return (word >> (bit & 31u)) & ((1u << l.BPB) - 1u);
-}
-
 struct TbArgs {
   const uint8_t* scratch;
   int64_t tile_stride, hdr_offset;
-  BpLayout lay;
+  RowLayout lay;
   int n, L, roll, write, cb;
   const int32_t* start;  // start edge per tile
   int64_t start_stride;
@@ -651,30 +616,7 @@ struct TbArgs {
 // and emit the edge reached (the tail-biting end state). write = 1: emit
 // every state and its codebook value.
 
-// Backpointer mode (K = 8): one thread per tile reads k from the row.
-__global__ void __launch_bounds__(256) traceback_bp_kernel(TbArgs a) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= a.n) return;
-  const BpLayout& lay = a.lay;
-  const int K = lay.K, KR = 16 - K, L = a.L;
-  const uint8_t* blk = a.scratch + (int64_t)t * a.tile_stride;
-  uint32_t edge = (uint32_t)a.start[(int64_t)t * a.start_stride] & ((65536u >> K) - 1u);
-  for (int i = L - 1; i >= 0; --i) {
-    int ri = i + a.roll;
-    if (ri >= L) ri -= L;
-    const uint32_t k = read_backpointer(blk + (int64_t)ri * lay.row_bytes, lay, edge);
-    const uint32_t sigma = (k << KR) | edge;
-    if (a.write) {
-      a.out_idx[(int64_t)t * L + ri] = (int16_t)(uint16_t)sigma;
-      a.out_w[(int64_t)t * L + ri] = (float)decode_state(a.cb, sigma);
-    }
-    edge = sigma >> K;
-    if (!a.write && ri == 0) break;
-  }
-  if (!a.write) a.end_out[(int64_t)t * a.end_stride] = (int32_t)edge;
-}
-
-// Cost-row mode: one 64-lane wave per tile. At step i with edge e the path's
+// One 64-lane wave per tile. At step i with edge e the path's
 // predecessor branch is the key minimum over k of
 // fma(dh, dh, C_{i-1}[(k << (16-2K)) | (e >> K)]) (lowest k among equal
 // costs), dh = fp16(value((k << (16-K)) | e) - w_i). If step i-1 is D > 0
@@ -1098,6 +1040,7 @@ template <int K>
 struct StreamShape {
   static constexpr int W = (K == 1 || K == 2) ? 4 : (K <= 4 ? 2 : 1);  // waves per group
   static constexpr int NG = (K == 1) ? 1 : (K == 2 ? 2 : (K <= 5 ? 4 : 8));
+  static_assert(K >= 1 && K <= 8, "cost-row bitrates");
   static constexpr int THREADS = 64 * (1 + W * NG);
 };
 
@@ -1114,8 +1057,11 @@ __global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kern
   constexpr int RV = 2 * (65536 >> K) / 16;  // 16-byte vectors per row
   constexpr int W = StreamShape<K>::W, NG = StreamShape<K>::NG;
   constexpr int NLT = 64 * W;                // threads per loader group
-  constexpr int V = RV / NLT;
-  static_assert(RV % NLT == 0 && V >= 1, "rows split evenly over a loader group");
+  // A row smaller than a loader group (K = 8: 32 vectors) leaves the
+  // group's threads lt >= RV idle.
+  constexpr bool PART = RV < NLT;
+  constexpr int V = PART ? 1 : RV / NLT;
+  static_assert(PART || RV % NLT == 0, "rows split evenly over a loader group");
   __shared__ u32x4 s_ring[2][RV];
   __shared__ uint16_t s_wbits[256];
   __shared__ uint16_t s_oidx[256];
@@ -1143,8 +1089,9 @@ __global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kern
 
   const int g = (wave - 1) / W;              // loader group (wave >= 1)
   const int lt = threadIdx.x - 64 - g * NLT;
+  const bool loads = wave > 0 && (!PART || lt < RV);
   u32x4 buf[V];  // native vectors: registers, not scratch
-  if (wave > 0) {
+  if (loads) {
     if (g < NR) {
       const u32x4* src = row_src(g);
 #pragma unroll
@@ -1187,7 +1134,7 @@ __global__ void __launch_bounds__(StreamShape<K>::THREADS) traceback_stream_kern
           }
         }
       }
-    } else {
+    } else if (loads) {
       const int j = q + 1;  // the row to place in the ring this iteration
       if (j < NR && j % NG == g) {
 #pragma unroll
@@ -1431,7 +1378,7 @@ static int validate_common(int K, int cb, int L) {
 
 static bool use_generic(int K, int generic) { return generic || !exl3::has_fast_kernel(K); }
 
-static BpLayout layout_for(int K) { return exl3::make_layout(K); }
+static RowLayout layout_for(int K) { return exl3::make_layout(K); }
 
 template <int K, int CB>
 static void launch_fast_cb(const FwdArgs& a, hipStream_t st) {
@@ -1462,6 +1409,7 @@ static int launch_forward(const FwdArgs& a, int K, int generic, hipStream_t st) 
       case 5: launch_fast<5>(a, st); break;
       case 6: launch_fast<6>(a, st); break;
       case 7: launch_fast<7>(a, st); break;
+      case 8: launch_fast<8>(a, st); break;
       default: return set_error("no fast kernel for K=%d", K);
     }
   }
@@ -1470,7 +1418,7 @@ static int launch_forward(const FwdArgs& a, int K, int generic, hipStream_t st) 
 
 static FwdArgs forward_args(const float* in, int n, int K, int cb, int L, uint8_t* scratch,
                             uint16_t* term_costs) {
-  const BpLayout lay = layout_for(K);
+  const RowLayout lay = layout_for(K);
   FwdArgs a{};
   a.in = in;
   a.n = n;
@@ -1480,7 +1428,6 @@ static FwdArgs forward_args(const float* in, int n, int K, int cb, int L, uint8_
   a.tile_stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
   a.hdr_offset = exl3::header_offset(lay, L);
   a.term_costs = term_costs;
-  a.store_rows = L;
   a.store_from = 0;
   return a;
 }
@@ -1521,27 +1468,22 @@ static void launch_traceback_rows(const TbArgs& a, hipStream_t st) {
 
 static int launch_traceback(const TbArgs& a, hipStream_t st) {
   if (a.n <= 0) return 0;
-  if (a.lay.mode == exl3::MODE_BACKPOINTERS) {
-    const int block = 256;
-    hipLaunchKernelGGL(traceback_bp_kernel, dim3((a.n + block - 1) / block), dim3(block), 0, st,
-                       a);
-  } else {
-    switch (a.lay.K) {
-      case 1: launch_traceback_rows<1>(a, st); break;
-      case 2: launch_traceback_rows<2>(a, st); break;
-      case 3: launch_traceback_rows<3>(a, st); break;
-      case 4: launch_traceback_rows<4>(a, st); break;
-      case 5: launch_traceback_rows<5>(a, st); break;
-      case 6: launch_traceback_rows<6>(a, st); break;
-      default: launch_traceback_rows<7>(a, st); break;
-    }
+  switch (a.lay.K) {
+    case 1: launch_traceback_rows<1>(a, st); break;
+    case 2: launch_traceback_rows<2>(a, st); break;
+    case 3: launch_traceback_rows<3>(a, st); break;
+    case 4: launch_traceback_rows<4>(a, st); break;
+    case 5: launch_traceback_rows<5>(a, st); break;
+    case 6: launch_traceback_rows<6>(a, st); break;
+    case 7: launch_traceback_rows<7>(a, st); break;
+    default: launch_traceback_rows<8>(a, st); break;
   }
   return check_launch("traceback");
 }
 
 static TbArgs traceback_args(const uint8_t* scratch, int n, int K, int cb, int L, int roll,
                              int write) {
-  const BpLayout lay = layout_for(K);
+  const RowLayout lay = layout_for(K);
   TbArgs t{};
   t.scratch = scratch;
   t.tile_stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
@@ -1588,7 +1530,7 @@ int64_t exl3_scratch_edges_bytes(int K, int L, int64_t tiles) {
 
 int64_t exl3_backpointer_slot(int K, int64_t edge) {
   if (K < 1 || K > 8 || edge < 0 || edge >= (65536 >> K)) return set_error("bad edge"), -1;
-  return exl3::bp_slot(layout_for(K), (uint32_t)edge);
+  return exl3::row_slot(layout_for(K), (uint32_t)edge);
 }
 
 int exl3_forward_pass(const float* in, uint16_t* temp_costs, uint8_t* temp_edges,
@@ -1641,7 +1583,7 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
   if (n <= 0) return set_error("num_tiles must be positive, got %lld", (long long)n);
   if (batch_cap < 1) return set_error("temp_costs batch dimension B must be >= 1");
   if (!in || !out_w || !out_idx || !temp_costs || !temp_edges) return set_error("NULL buffer");
-  const BpLayout lay = layout_for(K);
+  const RowLayout lay = layout_for(K);
   const int64_t stride = (int64_t)exl3::tile_scratch_bytes(lay, L);
   // Header row of each tile: int32 {pass-1 terminal edge, end state, ...}.
   const int64_t hstride = stride / 4;
@@ -1657,9 +1599,8 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
     FwdArgs a = forward_args(in + off * L, chunk, K, cb, L, temp_edges, temp_costs);
     // Pass 1: rotation L/2, unconstrained. The traceback covers ring rows
     // 0..L/2-1 only, i.e. forward steps L/2..L-1 (reference_encoder.py:284-288),
-    // so only those backpointer rows and the cost rows they need are stored.
+    // so only the cost rows those steps need are stored.
     a.roll = L / 2;
-    a.store_rows = L / 2;
     a.store_from = exl3::first_needed_row(lay, L);
     a.cost_slot = 0;
     a.best_edges = best_edges;
@@ -1673,7 +1614,6 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
     if (launch_traceback(t1, st)) return 1;
     // Pass 2: natural order, wrap constrained to the end state (:290-293).
     a.roll = 0;
-    a.store_rows = L;
     a.store_from = 0;
     a.pre_states = end_states;
     a.pre_stride = hstride;

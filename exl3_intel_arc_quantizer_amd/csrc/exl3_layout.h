@@ -11,10 +11,10 @@
 // unit of work the forward kernels assign to threads.
 //
 // The reference keeps, per (ring row, edge), the chosen predecessor edge as
-// int16 (quantize_kernels.sycl:124,153). Here the per-tile scratch holds one
-// of two things, chosen by K:
+// int16 (quantize_kernels.sycl:124,153). Here the per-tile scratch holds
+// cost rows at every K = 1..8:
 //
-// * cost rows (K = 1..7): the fp16 path-cost vector after a step (E * 2
+// * the fp16 path-cost vector after a step (E * 2
 //   bytes). The forward pass then only needs the minimum cost per edge, which
 //   packed fp16 arithmetic computes at the VALU roofline, and the traceback
 //   recomputes the 2^K candidates of the one edge on the path from the costs
@@ -24,19 +24,18 @@
 //   (K = 2..5 also keep part of the digit before beside it, see
 //   cost_row_pos).
 //   Only every row_stride(K)-th step is stored (8 KiB or less of HBM writes
-//   per step at K <= 5); for a step d rows past the last stored one, the
+//   per step at K <= 5, every step at K >= 6, where a row is 2 KiB or less);
+//   for a step d rows past the last stored one, the
 //   traceback rebuilds the costs it needs level by level, each a minimum
 //   over 2^K candidates, from 2^(K(d+1)) entries of the stored row. Stored
 //   step r sits in row slot r / stride, in step order (independent of the
 //   ring roll).
-// * backpointer rows (K = 8): the winning branch k per edge as one byte,
-//   since the predecessor is (k << (16-2K)) | (e >> K); row r holds ring
-//   row r.
 //
-// Per-tile block: tile_rows(K, L) rows of row_bytes; the last one is a
-// header: int32 [0] pass-1 terminal edge, [1] end state, [2] pre_state of
-// the last forward pass; from byte 16, L fp16 inputs in ring order (cost-row
-// mode), which the traceback reads.
+// Per-tile block: tile_rows(K, L) rows of row_bytes: the stored rows, then
+// the header (one row, two at K = 8 where a row is 512 bytes): int32 [0]
+// pass-1 terminal edge, [1] end state, [2] pre_state of the last forward
+// pass; from byte 16, the L fp16 inputs in ring order, which the traceback
+// reads.
 #pragma once
 
 #include <stdint.h>
@@ -49,21 +48,15 @@
 
 namespace exl3 {
 
-enum { MODE_BACKPOINTERS = 0, MODE_COST_ROWS = 1 };
-
-struct BpLayout {
+struct RowLayout {
   int32_t K;          // bitrate
-  int32_t mode;       // MODE_BACKPOINTERS or MODE_COST_ROWS
-  int32_t stride;     // cost rows: every stride-th step is stored
-  int32_t BPB;        // bits per field (16 in cost-row mode)
-  int32_t row_bytes;
+  int32_t stride;     // every stride-th step's cost row is stored
+  int32_t row_bytes;  // E fp16 costs
   int32_t reserved;
 };
 
-EXL3_HD inline bool uses_cost_rows(int K) { return K >= 1 && K <= 7; }
-
 // Steps between stored cost rows: about 8 KiB of HBM writes per step at
-// K <= 5, every step at K = 6, 7 (where a row is 2 KiB or less).
+// K <= 5, every step at K >= 6 (where a row is 2 KiB or less).
 EXL3_HD constexpr inline int row_stride(int K) {
   return K == 1 ? 8 : (K == 2 ? 4 : (K <= 5 ? 2 : 1));
 }
@@ -80,32 +73,29 @@ EXL3_HD constexpr inline int row_stride(int K) {
 //   5 :  1 2  1  32
 //   6 :  1 2  2  32
 //   7 :  1 2  4  32
-// K = 8 has a single group and runs on the generic kernel. Must match
-// FastShape in exl3_encoder.hip.
+//   8 :  1 2  8  32   (a single group: every edge reads all 256 costs)
+// Must match FastShape in exl3_encoder.hip.
 EXL3_HD inline int fast_G(int K) { return K == 1 ? 16 : (K == 2 ? 4 : 1); }
 EXL3_HD inline int fast_J(int K) {
   return K == 1 ? 2 : (K == 2 ? 4 : (K == 3 ? 8 : (K == 4 ? 4 : 2)));
 }
-EXL3_HD inline int fast_P(int K) { return K == 6 ? 2 : (K == 7 ? 4 : 1); }
-EXL3_HD inline bool has_fast_kernel(int K) { return K >= 1 && K <= 7; }
+EXL3_HD inline int fast_P(int K) { return K == 6 ? 2 : (K == 7 ? 4 : (K == 8 ? 8 : 1)); }
+EXL3_HD inline bool has_fast_kernel(int K) { return K >= 1 && K <= 8; }
 
 // Scratch layout of bitrate K (the same for every kernel variant, so the
 // split forward/backward passes may mix them).
-EXL3_HD inline BpLayout make_layout(int K) {
-  BpLayout l;
+EXL3_HD inline RowLayout make_layout(int K) {
+  RowLayout l;
   l.K = K;
-  const int E = 65536 >> K;
-  l.mode = uses_cost_rows(K) ? MODE_COST_ROWS : MODE_BACKPOINTERS;
-  l.stride = uses_cost_rows(K) ? row_stride(K) : 1;
-  l.BPB = uses_cost_rows(K) ? 16 : 8;
-  l.row_bytes = E * l.BPB / 8;
+  l.stride = row_stride(K);
+  l.row_bytes = (65536 >> K) * 2;
   l.reserved = 0;
   return l;
 }
 
-// Cost rows: which steps are stored, where, and where edge x sits in a row.
-EXL3_HD inline bool cost_row_stored(const BpLayout& l, int step) { return step % l.stride == 0; }
-EXL3_HD inline int cost_row_slot(const BpLayout& l, int step) { return step / l.stride; }
+// Which steps are stored, where, and where edge x sits in a row.
+EXL3_HD inline bool cost_row_stored(const RowLayout& l, int step) { return step % l.stride == 0; }
+EXL3_HD inline int cost_row_slot(const RowLayout& l, int step) { return step / l.stride; }
 // Group-major: x = (k << (16-2K)) | h at (h << K) | k, so the 2^K costs a
 // traceback step compares are one chunk. At K = 2..5, where a stored row
 // serves several steps and one traceback tree spans 2^(K * (stride + 1))
@@ -143,40 +133,41 @@ EXL3_HD inline uint32_t cost_row_edge(int K, uint32_t t) {
 }
 // First row the pass-1 traceback reaches: it covers steps L-1 .. L/2 and
 // needs the stored row at or before L/2 - 1.
-EXL3_HD inline int first_needed_row(const BpLayout& l, int L) {
+EXL3_HD inline int first_needed_row(const RowLayout& l, int L) {
   const int r = L / 2 - 1;
   return r - r % l.stride;
-}
-
-// Rows per tile: the stored steps 0, stride, ..., up to L - 2 (the
-// traceback never reads the costs after the last step) plus the header in
-// cost-row mode; L ring rows plus the header in backpointer mode.
-EXL3_HD inline int tile_rows(const BpLayout& l, int L) {
-  if (l.mode == MODE_COST_ROWS) return (L - 2) / l.stride + 2;
-  return L + 1;
-}
-
-EXL3_HD inline uint64_t tile_scratch_bytes(const BpLayout& l, int L) {
-  return (uint64_t)tile_rows(l, L) * (uint64_t)l.row_bytes;
-}
-
-// Byte offset of the header row inside a tile block.
-EXL3_HD inline int64_t header_offset(const BpLayout& l, int L) {
-  return (int64_t)(tile_rows(l, L) - 1) * l.row_bytes;
-}
-
-// Position of edge e inside a scratch row: group-major in cost-row mode,
-// the edge itself for the K = 8 backpointer bytes.
-EXL3_HD inline uint32_t bp_slot(const BpLayout& l, uint32_t e) {
-  if (l.mode == MODE_COST_ROWS) return cost_row_pos(l.K, e);
-  return e;
 }
 
 // Header row fields.
 constexpr int HDR_BEST_EDGE = 0;  // int32 index
 constexpr int HDR_END_STATE = 1;  // int32 index
 constexpr int HDR_PRE_STATE = 2;  // int32 index
-constexpr int HDR_W_BYTES = 16;   // byte offset of the L fp16 inputs (cost-row mode)
+constexpr int HDR_W_BYTES = 16;   // byte offset of the L fp16 inputs
+
+// Stored rows per tile: steps 0, stride, ..., up to L - 2 (the traceback
+// never reads the costs after the last step).
+EXL3_HD inline int stored_rows(const RowLayout& l, int L) { return (L - 2) / l.stride + 1; }
+
+// Header rows: the 16-byte fields and the L fp16 inputs.
+EXL3_HD inline int header_rows(const RowLayout& l, int L) {
+  return (HDR_W_BYTES + 2 * L + l.row_bytes - 1) / l.row_bytes;
+}
+
+EXL3_HD inline int tile_rows(const RowLayout& l, int L) {
+  return stored_rows(l, L) + header_rows(l, L);
+}
+
+EXL3_HD inline uint64_t tile_scratch_bytes(const RowLayout& l, int L) {
+  return (uint64_t)tile_rows(l, L) * (uint64_t)l.row_bytes;
+}
+
+// Byte offset of the header inside a tile block.
+EXL3_HD inline int64_t header_offset(const RowLayout& l, int L) {
+  return (int64_t)stored_rows(l, L) * l.row_bytes;
+}
+
+// Position of edge e inside a stored row.
+EXL3_HD inline uint32_t row_slot(const RowLayout& l, uint32_t e) { return cost_row_pos(l.K, e); }
 
 // tensor_core_perm (reference trellis_format.py:88-108): encoded element
 // 8t + s is original position row*16 + col with row in

@@ -15,9 +15,8 @@ is no CPU fallback.
 Deviations from the reference, all deliberate:
 
 * scratch layout: ``temp_edges`` is ``uint8 (B, ROWS, ROW)``: every
-  stride-th fp16 cost row (K = 1..7) or one backpointer byte per edge
-  (K = 8), plus a header row, see include/exl3_encoder.h; sized by the new
-  ScratchEstimator;
+  stride-th fp16 cost row, plus the header, see include/exl3_encoder.h;
+  sized by the new ScratchEstimator;
 * the arena's default batch capacity is 4096 tiles (the reference used 64 for
   the Arc iGPU), enough for eight waves of 1024-thread workgroups on 256 CUs;
 * traceback placement: ``gpu_resident`` runs the fused encoder;

@@ -1,22 +1,23 @@
-"""Scratch sizing for the MI355X encoder (cost-row / backpointer layout).
+"""Scratch sizing for the MI355X encoder (cost-row layout).
 
 Counterpart of exl3_quant/scratch_estimator.py:23-172 with the same class
 and method names. The formula changes with the layout
 (include/exl3_encoder.h, csrc/exl3_layout.h):
 
     S      = 65536 >> K                      edges per step
-    row    = S * 2                           K = 1..7: fp16 cost rows
-           = S                               K = 8: one backpointer byte per edge
-    rows   = (T - 2) // stride + 2           K = 1..7: every stride-th step
-                                             (stride 8, 4, 2, 2, 2, 1, 1) + header
-           = T + 1                           K = 8: T ring rows + header
+    row    = S * 2                           one fp16 cost per edge
+    rows   = (T - 2) // stride + 1           every stride-th step
+                                             (stride 8, 4, 2, 2, 2, 1, 1, 1)
+           + ceil((16 + 2 T) / row)          header: fields and the T inputs
+                                             (one row; two at K = 8)
     costs  = B * 2 * S * 2                   terminal fp16 costs of both passes
     edges  = B * rows * row
 
 The reference's int16 layout, ``B * T * S * 2``, is still available by
 passing ``bytes_per_edge`` explicitly (e.g. to compare the two). Per tile at
 T = 256: K=1 2.06 MiB (reference 16 MiB), K=2 2.03 MiB (8 MiB), K=3 2.02 MiB
-(4 MiB), K=4 1.01 MiB (2 MiB), K=5 516 KiB (1 MiB), K=6 514 KiB (512 KiB).
+(4 MiB), K=4 1.01 MiB (2 MiB), K=5 516 KiB (1 MiB), K=6 512 KiB (512 KiB),
+K=7 256 KiB (256 KiB), K=8 128.5 KiB (128 KiB).
 """
 
 from __future__ import annotations
@@ -33,9 +34,12 @@ BYTES_PER_MB = 1000 ** 2
 BYTES_PER_GB = 1000 ** 3
 
 
+HEADER_FIELD_BYTES = 16  # int32 terminal edge, end state, pre_state, spare
+
+
 def uses_cost_rows(k: int) -> bool:
-    """K = 1..7 keep fp16 cost rows; K = 8 keeps one backpointer byte per edge."""
-    return 1 <= k <= 7
+    """Every supported bitrate (K = 1..8) keeps fp16 cost rows."""
+    return 1 <= k <= 8
 
 
 def row_stride(k: int) -> int:
@@ -44,8 +48,9 @@ def row_stride(k: int) -> int:
 
 
 def backpointer_bits(k: int) -> int:
-    """Bits stored per edge and row (exl3_layout.h make_layout)."""
-    return 16 if uses_cost_rows(k) else 8
+    """Bits stored per edge and row: one fp16 cost (exl3_layout.h make_layout).
+    The name is the reference's; this encoder stores costs, not backpointers."""
+    return 16
 
 
 def backpointer_row_bytes(k: int) -> int:
@@ -55,9 +60,9 @@ def backpointer_row_bytes(k: int) -> int:
 
 def tile_rows(k: int, t: int = 256) -> int:
     """Scratch rows per tile, header included (exl3_layout.h tile_rows)."""
-    if uses_cost_rows(k):
-        return (t - 2) // row_stride(k) + 2
-    return t + 1
+    row = backpointer_row_bytes(k)
+    header = -(-(HEADER_FIELD_BYTES + 2 * t) // row)
+    return (t - 2) // row_stride(k) + 1 + header
 
 
 @dataclass(frozen=True)

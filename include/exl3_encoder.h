@@ -21,17 +21,17 @@
  * Scratch ("temp_costs" / "temp_edges" in the reference) has a new layout:
  *   temp_costs : fp16 [B][2][E]           terminal path costs of pass 1 / 2,
  *                                          E = 65536 >> K (same as reference)
- *   temp_edges : bytes [B][ROWS][ROWB]    per tile, K = 1..7: the fp16 path
- *                                          costs after every S-th step
- *                                          (S = 8, 4, 2, 2, 2, 1, 1 for
- *                                          K = 1..7; ROWB = 2E, group-major),
- *                                          K = 8: one backpointer byte per
- *                                          edge and ring row (ROWB = E); plus
- *                                          a header row.
+ *   temp_edges : bytes [B][ROWS][ROWB]    per tile, the fp16 path costs
+ *                                          after every S-th step
+ *                                          (S = 8, 4, 2, 2, 2, 1, 1, 1 for
+ *                                          K = 1..8; ROWB = 2E, group-major),
+ *                                          then the header (the L inputs and
+ *                                          three int32 fields).
  * where B is the number of tiles the scratch holds (the reference's batch
  * capacity). exl3_scratch_row_bytes() gives ROWB and
- * exl3_scratch_edges_bytes(K, L, 1) / ROWB gives ROWS ((L - 2) / S + 2 in
- * cost-row mode, L + 1 at K = 8). The traceback recomputes the branch of the
+ * exl3_scratch_edges_bytes(K, L, 1) / ROWB gives ROWS ((L - 2) / S + 1
+ * stored rows plus one header row, two at K = 8 where ROWB = 512). The
+ * traceback recomputes the branch of the
  * path at each step from the stored costs. The reference layout stored int16
  * predecessor edges, [B][L][E] (quantize_xpu.cpp:153-157).
  */
@@ -70,8 +70,8 @@ int64_t exl3_scratch_row_bytes(int K);
  * ScratchEstimator.estimate_scratch, scratch_estimator.py:77-112). */
 int64_t exl3_scratch_edges_bytes(int K, int L, int64_t tiles);
 
-/* Position of `edge` inside a scratch row: (h << K) | k for
- * edge = (k << (16 - 2K)) | h in cost-row mode, edge itself at K = 8
+/* Position of `edge` inside a stored cost row: (h << K) | k for
+ * edge = (k << (16 - 2K)) | h, with part of the digit before at K = 2..5
  * (exposed for host-side checks). */
 int64_t exl3_backpointer_slot(int K, int64_t edge);
 
@@ -109,8 +109,8 @@ int exl3_quantize_tiles_noalloc(const float* in, float* out_w, int16_t* out_idx,
 /* Replaces quantize_tiles_forward_pass (quantize_xpu.cpp:169-215,
  * quantize_kernels.sycl:658-704): one forward add-compare-select pass over
  * the ring with rotation `roll`; tile t is constrained to start from edge
- * pre_states[t] when that is >= 0. Writes every stored cost row (or, at
- * K = 8, all L backpointer rows), the tile header and the terminal costs to
+ * pre_states[t] when that is >= 0. Writes every stored cost row, the tile
+ * header and the terminal costs to
  * temp_costs[t][cost_slot]. n <= batch capacity. generic = 1 selects the
  * reference-structured kernel. */
 int exl3_forward_pass(const float* in, uint16_t* temp_costs, uint8_t* temp_edges,

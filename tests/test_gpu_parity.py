@@ -7,8 +7,6 @@ Run on an MI355X:  python -u -m pytest tests -m gpu -x -v --timeout 120
 
 from __future__ import annotations
 
-import hashlib
-
 import numpy as np
 import pytest
 
@@ -142,33 +140,37 @@ def test_other_golden_sets(name):
                 np.testing.assert_array_equal(bd.packed, g["packed"][sel][:, :16 * int(K)])
 
 
-def _pred_table(temp_edges_row_block, K, L):
-    """Decode one tile's backpointer rows (K = 8) into the reference's
-    predecessor-edge table (L, E) uint16."""
-    from exl3_intel_arc_quantizer_amd import _native
-    from exl3_intel_arc_quantizer_amd.scratch_estimator import backpointer_bits
-    lib = _native.load_library()
+def _check_stored_rows(block, tile16, K, roll, pre):
+    """One tile's scratch block against the C oracle's forward pass: every
+    stored cost row (the step after every stride-th step, at the positions
+    exl3_backpointer_slot reports) and the header (pre_state, the fp16
+    inputs in ring order)."""
+    from exl3_intel_arc_quantizer_amd._native import load_library
+    from exl3_intel_arc_quantizer_amd.scratch_estimator import row_stride, tile_rows
     E = 65536 >> K
-    bpb = backpointer_bits(K)
-    slots = np.array([lib.exl3_backpointer_slot(K, e) for e in range(E)], dtype=np.int64)
-    rows = temp_edges_row_block[:L]
-    bits = slots * bpb
-    byte = rows[:, bits // 8].astype(np.int64)
-    k = (byte >> (bits % 8)) & ((1 << bpb) - 1)
-    e = np.arange(E)
-    return ((k << (16 - 2 * K)) | (e >> K)).astype(np.uint16)
+    _, _, want_rows = c_oracle.forward_pass(tile16, K=K, cb=2, roll=roll, pre_state=pre,
+                                            with_rows=True)
+    lib = load_library()
+    pos = np.array([lib.exl3_backpointer_slot(K, e) for e in range(E)], dtype=np.int64)
+    stride = row_stride(K)
+    stored = 254 // stride + 1
+    assert block.shape[0] == tile_rows(K) and block.shape[1] == 2 * E
+    for r in range(0, 255, stride):
+        got = block[r // stride].view(np.uint16)
+        np.testing.assert_array_equal(got[pos], want_rows[r], err_msg=f"K={K} row {r}")
+    hdr = block[stored:].reshape(-1)
+    np.testing.assert_array_equal(hdr[16:16 + 512].view(np.uint16), tile16.view(np.uint16))
+    assert int(hdr[8:12].view(np.int32)[0]) == pre
 
 
 @pytest.mark.parametrize("generic", [False, True])
 def test_forward_pass_pins(ext, torch_mod, generic):
     """Split forward pass (quantize_xpu.cpp:169-215) against the reference's
-    forward(): terminal costs bit-exact; in cost-row mode (K = 1..7) every
-    stored cost row (every stride-th step, group-major positions) against
-    the C oracle's per-step costs; in backpointer mode (K = 8) the full
-    predecessor table against its hash. Then the split backward pass, which
-    rebuilds the unstored steps, reaches the reference's end state."""
-    from exl3_intel_arc_quantizer_amd._native import edges_shape, load_library
-    from exl3_intel_arc_quantizer_amd.scratch_estimator import row_stride, uses_cost_rows
+    forward(): terminal costs bit-exact; every stored cost row (every
+    stride-th step, group-major positions) against the C oracle's per-step
+    costs; the header's inputs and pre_state. Then the split backward pass,
+    which rebuilds the unstored steps, reaches the reference's end state."""
+    from exl3_intel_arc_quantizer_amd._native import edges_shape
     g = load_golden("forward_pass")
     for i in range(4):
         K, roll, pre, best, end = (int(v) for v in g[f"case{i}_meta"])
@@ -189,47 +191,43 @@ def test_forward_pass_pins(ext, torch_mod, generic):
         torch_mod.cuda.synchronize()
         np.testing.assert_array_equal(costs[0, 1].cpu().numpy().view(np.uint16),
                                       g[f"case{i}_costs"])
-        block = edges[0].cpu().numpy()
-        if uses_cost_rows(K):
-            _, _, want_rows = c_oracle.forward_pass(tile16, K=K, cb=2, roll=roll, pre_state=pre,
-                                                    with_rows=True)
-            lib = load_library()
-            pos = np.array([lib.exl3_backpointer_slot(K, e) for e in range(E)], dtype=np.int64)
-            stride = row_stride(K)
-            assert block.shape[0] == 254 // stride + 2
-            for r in range(0, 255, stride):
-                got = block[r // stride].view(np.uint16)
-                np.testing.assert_array_equal(got[pos], want_rows[r], err_msg=f"row {r}")
-            hdr = block[-1]
-            np.testing.assert_array_equal(hdr[16:16 + 512].view(np.uint16), tile16.view(np.uint16))
-            assert int(hdr[8:12].view(np.int32)[0]) == pre
-        else:
-            table = _pred_table(block, K, 256)
-            np.testing.assert_array_equal(table[:4, :64], g[f"case{i}_edges_head"])
-            assert hashlib.sha256(table.tobytes()).hexdigest() == str(g[f"case{i}_edges_sha256"])
+        _check_stored_rows(edges[0].cpu().numpy(), tile16, K, roll, pre)
         assert int(ends.item()) == end
 
 
-def test_backpointer_rows_k8(ext, torch_mod):
-    """K = 8 keeps one backpointer byte per edge and ring row: the decoded
-    predecessor table and terminal costs of a forward pass equal the C
-    oracle's (reference forward(), reference_encoder.py:130-204), for an
-    unconstrained and a constrained pass."""
+@pytest.mark.parametrize("generic", [False, True])
+def test_cost_rows_k8(ext, torch_mod, generic):
+    """K = 8 stores its cost row after every step (512 bytes) and a two-row
+    header: every row, the terminal costs and the header equal the C
+    oracle's forward pass (reference forward(), reference_encoder.py:130-204)
+    for an unconstrained and a constrained pass, from the fast kernel and the
+    reference-structured one; the split backward pass then reaches the
+    oracle's end state."""
     from exl3_intel_arc_quantizer_amd._native import edges_shape
     rng = np.random.default_rng(88)
     tile16 = rng.normal(0.0, 1.1, size=256).astype(np.float16)
     x = torch_mod.from_numpy(tile16.astype(np.float32)).cuda().reshape(1, 256)
+    ref = c_oracle.encode_tiles(tile16.astype(np.float32)[None], K=8, cb=2)
     for roll, pre in ((128, -1), (0, 77)):
-        print(f"K=8 forward roll={roll} pre={pre}", flush=True)
+        print(f"K=8 forward roll={roll} pre={pre} generic={generic}", flush=True)
         costs = torch_mod.zeros((1, 2, 256), dtype=torch_mod.float16, device="cuda")
         edges = torch_mod.zeros(edges_shape(1, 8), dtype=torch_mod.uint8, device="cuda")
         pre_t = torch_mod.full((1,), pre, dtype=torch_mod.int32, device="cuda")
-        ext.quantize_tiles_forward_pass(x, costs, edges, pre_t, 8, False, True, roll, 0)
+        ext.quantize_tiles_forward_pass(x, costs, edges, pre_t, 8, False, True, roll, 0, 32,
+                                        generic)
         torch_mod.cuda.synchronize()
-        want_edges, want_costs = c_oracle.forward_pass(tile16, K=8, cb=2, roll=roll, pre_state=pre)
-        np.testing.assert_array_equal(_pred_table(edges[0].cpu().numpy(), 8, 256), want_edges)
+        _, want_costs = c_oracle.forward_pass(tile16, K=8, cb=2, roll=roll, pre_state=pre)
         np.testing.assert_array_equal(costs[0, 0].cpu().numpy().view(np.uint16),
                                       want_costs.view(np.uint16))
+        _check_stored_rows(edges[0].cpu().numpy(), tile16, 8, roll, pre)
+        if pre < 0:
+            ends = torch_mod.zeros((1,), dtype=torch_mod.int32, device="cuda")
+            w = torch_mod.zeros((1, 256), dtype=torch_mod.float32, device="cuda")
+            idx = torch_mod.zeros((1, 256), dtype=torch_mod.int16, device="cuda")
+            ext.quantize_tiles_backward_pass(costs, edges, w, idx, ends, 1, 8, False, True, roll,
+                                             0, False)
+            torch_mod.cuda.synchronize()
+            assert int(ends.item()) == int(ref.end_state[0])
 
 
 def test_usm_host_entry_point(ext, torch_mod):
@@ -308,7 +306,7 @@ def test_tile_encoder_nan_rejection(torch_mod):
         enc.encoder.arena.release()
 
 
-@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_traceback_kernels_agree(K):
     """The two cost-row tracebacks (per-row tree loads, whole rows streamed
     through LDS) give the oracle's states in both passes, through the fused

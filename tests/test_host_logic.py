@@ -29,11 +29,12 @@ def test_reference_formula_fixtures_still_reproducible():
         assert a.costs_mib == pytest.approx(costs_mib)
 
 
-# Stored cost rows (every stride-th of steps 0..254) plus the header row, of
-# E * 2 bytes; K = 8: 256 ring rows plus the header, E bytes each.
+# Stored cost rows (every stride-th of steps 0..254) plus the header, rows of
+# E * 2 bytes; the header (16 bytes and 256 fp16 inputs) takes one row, two at
+# K = 8 where a row is 512 bytes.
 @pytest.mark.parametrize("k,per_tile", [(1, 33 * 65536), (2, 65 * 32768), (3, 129 * 16384),
                                         (4, 129 * 8192), (5, 129 * 4096), (6, 256 * 2048),
-                                        (7, 256 * 1024), (8, 257 * 256)])
+                                        (7, 256 * 1024), (8, 257 * 512)])
 def test_layout_formula(k, per_tile):
     a = ScratchEstimator.estimate_scratch(k=k, t=256, b=10)
     assert a.edges_bytes == 10 * per_tile
