@@ -409,7 +409,7 @@ __device__ __forceinline__ u16x2 group_min_u16x2(u16x2 v) {
   return v;
 }
 
-// Cost-row forward pass (K = 1..7): minimum cost per edge, rows to HBM.
+// Cost-row forward pass (K = 1..8): minimum cost per edge, rows to HBM.
 // Thread `unit` owns edges jj*J .. jj*J + J - 1 of G groups (one group, or
 // NV runs of GV consecutive groups when G > 1), in packed pairs (j, j + 1), and the Q = 2^K / P branches k = q*P + p of
 // lane p of its P-lane group (interleaved, so the group's LDS reads fall in
