@@ -26,7 +26,7 @@ extern "C" {
 int exl3_hadamard128(const float* in, float* out, int64_t rows, int64_t cols, int side,
                      void* stream);
 
-/* The two fused steps of regularize (regularize.py:159-173): each divides
+/* The two fused steps of regularize (regularize.py:171-181): each divides
  * the matrix by a scale vector and applies the blockwise Hadamard transform
  * in one pass over HBM, the arithmetic of a division (correctly rounded
  * fp32) followed by exl3_hadamard128.
