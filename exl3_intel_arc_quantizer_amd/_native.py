@@ -31,7 +31,7 @@ _SIGNATURES = {
     "exl3_decode_codebook": (_c_int, [_c_int, _c_vp, _c_vp]),
     "exl3_scratch_row_bytes": (_c_i64, [_c_int]),
     "exl3_scratch_edges_bytes": (_c_i64, [_c_int, _c_int, _c_i64]),
-    "exl3_backpointer_slot": (_c_i64, [_c_int, _c_i64]),
+    "exl3_cost_row_slot": (_c_i64, [_c_int, _c_i64]),
     "exl3_quantize_tiles": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int,
                                      _c_int, _c_int, _c_int, _c_i64, _c_vp]),
     "exl3_quantize_tiles_noalloc": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,

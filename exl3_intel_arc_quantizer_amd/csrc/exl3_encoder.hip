@@ -1528,7 +1528,7 @@ int64_t exl3_scratch_edges_bytes(int K, int L, int64_t tiles) {
   return (int64_t)exl3::tile_scratch_bytes(layout_for(K), L) * tiles;
 }
 
-int64_t exl3_backpointer_slot(int K, int64_t edge) {
+int64_t exl3_cost_row_slot(int K, int64_t edge) {
   if (K < 1 || K > 8 || edge < 0 || edge >= (65536 >> K)) return set_error("bad edge"), -1;
   return exl3::row_slot(layout_for(K), (uint32_t)edge);
 }

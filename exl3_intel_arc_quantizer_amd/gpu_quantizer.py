@@ -43,7 +43,7 @@ from . import build as _build
 from ._native import QuantizeExtension, load_library
 from .memory_policy import MemoryPolicy, MemoryPressureError, capture_snapshot
 from .reference_encoder import EncodingResult
-from .scratch_estimator import ScratchEstimator, backpointer_row_bytes, tile_rows
+from .scratch_estimator import ScratchEstimator, scratch_row_bytes, tile_rows
 from .trellis_format import (CB_3INST, CB_MCG, CB_MUL1, codebook_lut, tensor_core_perm,
                              tensor_core_perm_inv)
 
@@ -237,7 +237,7 @@ class ScratchArena:
 
         cand_b = target_b
         last_err: Optional[Exception] = None
-        rb = backpointer_row_bytes(k)
+        rb = scratch_row_bytes(k)
         while cand_b >= 1:
             est = ScratchEstimator.estimate_scratch(k=k, b=cand_b, t=tile_len)
             snap = capture_snapshot(self.device_index)

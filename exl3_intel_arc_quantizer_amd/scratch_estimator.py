@@ -47,20 +47,17 @@ def row_stride(k: int) -> int:
     return {1: 8, 2: 4, 3: 2, 4: 2, 5: 2}.get(k, 1)
 
 
-def backpointer_bits(k: int) -> int:
-    """Bits stored per edge and row: one fp16 cost (exl3_layout.h make_layout).
-    The name is the reference's; this encoder stores costs, not backpointers."""
-    return 16
+COST_BITS = 16  # one fp16 cost per edge and stored row
 
 
-def backpointer_row_bytes(k: int) -> int:
-    """Bytes of one scratch row (exl3_scratch_row_bytes)."""
-    return (65536 >> k) * backpointer_bits(k) // 8
+def scratch_row_bytes(k: int) -> int:
+    """Bytes of one scratch row (exl3_scratch_row_bytes): E fp16 costs."""
+    return (65536 >> k) * COST_BITS // 8
 
 
 def tile_rows(k: int, t: int = 256) -> int:
     """Scratch rows per tile, header included (exl3_layout.h tile_rows)."""
-    row = backpointer_row_bytes(k)
+    row = scratch_row_bytes(k)
     header = -(-(HEADER_FIELD_BYTES + 2 * t) // row)
     return (t - 2) // row_stride(k) + 1 + header
 
@@ -129,8 +126,8 @@ class ScratchEstimator:
         if bytes_per_edge is None:
             if k > 8:
                 raise ValueError(f"the encoder supports K in 1..8, got {k}")
-            bits = backpointer_bits(k)
-            edges_bytes = b * tile_rows(k, t) * backpointer_row_bytes(k)
+            bits = COST_BITS
+            edges_bytes = b * tile_rows(k, t) * scratch_row_bytes(k)
         else:
             bits = 8 * bytes_per_edge
             edges_bytes = b * t * states * bytes_per_edge

@@ -73,7 +73,7 @@ int64_t exl3_scratch_edges_bytes(int K, int L, int64_t tiles);
 /* Position of `edge` inside a stored cost row: (h << K) | k for
  * edge = (k << (16 - 2K)) | h, with part of the digit before at K = 2..5
  * (exposed for host-side checks). */
-int64_t exl3_backpointer_slot(int K, int64_t edge);
+int64_t exl3_cost_row_slot(int K, int64_t edge);
 
 /* Replaces quantize_tiles (quantize_xpu.cpp:112-167,
  * quantize_kernels.sycl:603-656): full two-pass tail-biting encode of n

@@ -143,7 +143,7 @@ def test_other_golden_sets(name):
 def _check_stored_rows(block, tile16, K, roll, pre):
     """One tile's scratch block against the C oracle's forward pass: every
     stored cost row (the step after every stride-th step, at the positions
-    exl3_backpointer_slot reports) and the header (pre_state, the fp16
+    exl3_cost_row_slot reports) and the header (pre_state, the fp16
     inputs in ring order)."""
     from exl3_intel_arc_quantizer_amd._native import load_library
     from exl3_intel_arc_quantizer_amd.scratch_estimator import row_stride, tile_rows
@@ -151,7 +151,7 @@ def _check_stored_rows(block, tile16, K, roll, pre):
     _, _, want_rows = c_oracle.forward_pass(tile16, K=K, cb=2, roll=roll, pre_state=pre,
                                             with_rows=True)
     lib = load_library()
-    pos = np.array([lib.exl3_backpointer_slot(K, e) for e in range(E)], dtype=np.int64)
+    pos = np.array([lib.exl3_cost_row_slot(K, e) for e in range(E)], dtype=np.int64)
     stride = row_stride(K)
     stored = 254 // stride + 1
     assert block.shape[0] == tile_rows(K) and block.shape[1] == 2 * E

@@ -15,7 +15,7 @@ from exl3_intel_arc_quantizer_amd.memory_policy import (
     BYTES_PER_GIB, MemoryPolicy, MemoryPressureError, capture_snapshot, default_reserve_bytes,
     read_system_memory, reflect_outstanding_counters)
 from exl3_intel_arc_quantizer_amd.scratch_estimator import (
-    BYTES_PER_MIB, ScratchEstimator, backpointer_bits, backpointer_row_bytes)
+    BYTES_PER_MIB, COST_BITS, ScratchEstimator, scratch_row_bytes)
 from oracle import trellis_format_ref
 
 
@@ -40,8 +40,8 @@ def test_layout_formula(k, per_tile):
     assert a.edges_bytes == 10 * per_tile
     assert a.costs_bytes == 10 * 2 * (65536 >> k) * 2
     assert a.total_bytes == a.costs_bytes + a.edges_bytes
-    assert backpointer_row_bytes(k) * 8 == (65536 >> k) * backpointer_bits(k)
-    assert backpointer_bits(k) >= k
+    assert scratch_row_bytes(k) * 8 == (65536 >> k) * COST_BITS
+    assert a.bits_per_edge == COST_BITS
 
 
 def test_estimator_validation_and_max_batch():

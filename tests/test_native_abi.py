@@ -46,26 +46,26 @@ def test_version_and_empty_error():
 @pytest.mark.parametrize("K", range(1, 9))
 def test_row_bytes_match_estimator(K):
     lib = _native.load_library()
-    assert lib.exl3_scratch_row_bytes(K) == scratch_estimator.backpointer_row_bytes(K)
+    assert lib.exl3_scratch_row_bytes(K) == scratch_estimator.scratch_row_bytes(K)
     for L in (256, 160):
         assert (lib.exl3_scratch_edges_bytes(K, L, 3)
                 == scratch_estimator.ScratchEstimator.estimate_scratch(k=K, t=L, b=3).edges_bytes)
 
 
 @pytest.mark.parametrize("K", range(1, 9))
-def test_backpointer_slots_are_a_permutation(K):
+def test_cost_row_slots_are_a_permutation(K):
     """Every edge owns exactly one backpointer field of a row."""
     lib = _native.load_library()
     E = 65536 >> K
     step = max(1, E // 4096)
     edges = np.arange(0, E, step)
-    slots = np.array([lib.exl3_backpointer_slot(K, int(e)) for e in edges])
+    slots = np.array([lib.exl3_cost_row_slot(K, int(e)) for e in edges])
     assert slots.min() >= 0 and slots.max() < E
     if step == 1:
         assert np.array_equal(np.sort(slots), np.arange(E))
     else:
         assert np.unique(slots).size == edges.size
-    assert lib.exl3_backpointer_slot(K, E) == -1
+    assert lib.exl3_cost_row_slot(K, E) == -1
 
 
 @pytest.mark.parametrize("K", [1, 6, 7])
@@ -76,7 +76,7 @@ def test_cost_row_positions_are_group_major(K):
     rng = np.random.default_rng(K)
     for x in rng.integers(0, 65536 >> K, size=64):
         k, h = int(x) >> ks, int(x) & ((1 << ks) - 1)
-        assert lib.exl3_backpointer_slot(K, int(x)) == (h << K) | k
+        assert lib.exl3_cost_row_slot(K, int(x)) == (h << K) | k
 
 
 def _predecessors(edges, K):
@@ -96,7 +96,7 @@ def test_cost_rows_keep_traceback_trees_together(K, stride, run):
     (the forward pass stores both from one dword read)."""
     lib = _native.load_library()
     E = 65536 >> K
-    pos = np.array([lib.exl3_backpointer_slot(K, x) for x in range(E)])
+    pos = np.array([lib.exl3_cost_row_slot(K, x) for x in range(E)])
     assert np.array_equal(np.sort(pos), np.arange(E))
     edge_at = np.argsort(pos)
     assert np.array_equal(edge_at[E // 2:], edge_at[:E // 2] + 1)
