@@ -54,7 +54,7 @@ def test_row_bytes_match_estimator(K):
 
 @pytest.mark.parametrize("K", range(1, 9))
 def test_cost_row_slots_are_a_permutation(K):
-    """Every edge owns exactly one backpointer field of a row."""
+    """Every edge owns exactly one cost position of a stored row."""
     lib = _native.load_library()
     E = 65536 >> K
     step = max(1, E // 4096)
