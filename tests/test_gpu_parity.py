@@ -140,6 +140,36 @@ def test_other_golden_sets(name):
                 np.testing.assert_array_equal(bd.packed, g["packed"][sel][:, :16 * int(K)])
 
 
+@pytest.mark.parametrize("K", [1, 5, 6, 7, 8])
+def test_l160_against_oracle(K):
+    """L = 160 at the bitrates the golden set (K = 2, 3, 4) leaves out: the
+    stored-row count, the header's place (one row at every K for L = 160,
+    where K = 8's 512-byte rows need two at L = 256) and the ring walk,
+    against the C oracle, through both traceback kernels."""
+    from exl3_intel_arc_quantizer_amd import _native
+    rng = np.random.default_rng(160 + K)
+    tiles = rng.normal(0.0, 1.0, size=(5, 160)).astype(np.float32)
+    tiles[2] *= 3.0
+    ref = c_oracle.encode_tiles(tiles, K=K, cb=2, pre_permute=False)
+    prev = _native.set_traceback_policy("auto")
+    try:
+        for policy in ("rows", "stream"):
+            _native.set_traceback_policy(policy)
+            print(f"L=160 K={K} traceback={policy}", flush=True)
+            enc = _encoder(K=K, cb=2, tile_len=160)
+            try:
+                bd = enc.encode_batch_detailed(tiles, pre_permute=False)
+            finally:
+                enc.arena.release()
+            np.testing.assert_array_equal(bd.output_indices, ref.output_indices, err_msg=policy)
+            np.testing.assert_array_equal(bd.end_states, ref.end_state, err_msg=policy)
+            np.testing.assert_array_equal(bd.path_costs, ref.path_cost, err_msg=policy)
+            np.testing.assert_array_equal(bd.reconstructed_perm, ref.reconstructed_perm,
+                                          err_msg=policy)
+    finally:
+        _native.set_traceback_policy(prev)
+
+
 def _check_stored_rows(block, tile16, K, roll, pre):
     """One tile's scratch block against the C oracle's forward pass: every
     stored cost row (the step after every stride-th step, at the positions
