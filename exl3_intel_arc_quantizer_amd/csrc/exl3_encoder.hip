@@ -421,10 +421,14 @@ __device__ __forceinline__ u16x2 group_min_u16x2(u16x2 v) {
 // IEEE minimum returns the same bits as an integer minimum). The pair minima
 // are in edge order for 32-bit LDS stores. CB is the codebook selector
 // (compile time keeps the prologue's registers low). Eight waves per SIMD:
-// two workgroups per CU where LDS allows (K >= 2), which caps VGPRs at 64;
-// K = 1 needs 128 KiB of LDS and runs one workgroup per CU.
-template <int K, int G, int J, int P, int CB>
-__global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdArgs a) {
+// two workgroups per CU, which caps VGPRs at 64. K = 1's ping-pong pair
+// of cost vectors takes 128 KiB of LDS, one workgroup per CU; INPLACE keeps
+// one vector (64 KiB) and updates it in place, with a second barrier per
+// step between the reads and the writes: two workgroups per CU, 10 % faster
+// at 1024 tiles and more, 3 % slower where one workgroup per CU is all the
+// batch fills.
+template <int K, int G, int J, int P, int CB, bool INPLACE>
+__global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forward_rows(FwdArgs a) {
   using C = FastCfg<K, G, J, P>;
   constexpr int JP = J / 2;
   constexpr int KS = 16 - 2 * K;
@@ -436,7 +440,8 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
   constexpr int EP = C::E + (1 << K) * PAD;         // padded vector length
   static_assert(C::Q % 2 == 0, "branches are folded two at a time");
   static_assert(PAD == 0 || G == 1, "padding keeps group pairs of G > 1 together");
-  __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][EP];
+  static_assert(!INPLACE || K == 1, "the in-place update is written for K = 1");
+  __shared__ __attribute__((aligned(16))) uint16_t s_cost[INPLACE ? 1 : 2][EP];
   __shared__ __attribute__((aligned(4))) f16 s_w[256];
   __shared__ uint32_t s_red[16];
 
@@ -478,12 +483,44 @@ __global__ void __launch_bounds__(1024, (K == 1 ? 4 : 8)) acs_forward_rows(FwdAr
   // every LDS address is a per-thread base plus an immediate offset.
   auto step = [&](auto phase, int i, f16 w) {
     constexpr int B = decltype(phase)::value;
-    const uint16_t* cin = s_cost[B];
-    uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[B ^ 1]);
+    const uint16_t* cin = s_cost[INPLACE ? 0 : B];
+    uint32_t* cout = reinterpret_cast<uint32_t*>(s_cost[INPLACE ? 0 : B ^ 1]);
     const bool store = i >= 1 && stores_row_at<K, B>(a, i);
     f16x2 w2;
     w2.x = w;
     w2.y = w;
+    if constexpr (INPLACE) {
+      static_assert(C::Q == 2 && P == 1 && JP == 1 && G % 2 == 0, "K = 1 shape");
+      // Both predecessor costs (k = 0, 1) of every group are read, and the
+      // stored row gathered, before the barrier; the new costs after it.
+      uint32_t cw[2][G / 2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int g2 = 0; g2 < G / 2; ++g2)
+          cw[b][g2] = *reinterpret_cast<const uint32_t*>(cin + b * SP + grp(2 * g2));
+      if (store) RowGather<K, C::NT, KS, PAD>::store(a, cin, i - 1);
+      __syncthreads();
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        f16x2 cv[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const f16x2 pair = __builtin_bit_cast(f16x2, cw[b][g >> 1]);
+          cv[b] = (g & 1) ? __builtin_shufflevector(pair, pair, 1, 1)
+                          : __builtin_shufflevector(pair, pair, 0, 0);
+        }
+        const f16x2 d0 = cbv[g][0][0] - w2;
+        const f16x2 d1 = cbv[g][0][1] - w2;
+        const f16x2 e0 = __builtin_elementwise_fma(d0, d0, cv[0]);
+        const f16x2 e1 = __builtin_elementwise_fma(d1, d1, cv[1]);
+        const int e = (grp(g) << K) | (jj * J);
+        cout[lds_pos<KS, PAD>(e) >> 1] =
+            __builtin_bit_cast(uint32_t, __builtin_elementwise_minimum(e0, e1));
+      }
+      __syncthreads();
+      return;
+    }
 
     f16x2 m[G][JP];
 #pragma unroll
@@ -1380,11 +1417,32 @@ static bool use_generic(int K, int generic) { return generic || !exl3::has_fast_
 
 static RowLayout layout_for(int K) { return exl3::make_layout(K); }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <int K, int CB>
 static void launch_fast_cb(const FwdArgs& a, hipStream_t st) {
   using Sh = FastShape<K>;
-  hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB>), dim3(a.n), dim3(1024), 0, st,
-                     a);
+  if (K == 1 && a.n > device_cus()) {
+    // More than one workgroup per CU to place: the in-place variant fits two.
+    hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB, K == 1>), dim3(a.n),
+                       dim3(1024), 0, st, a);
+    return;
+  }
+  hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB, false>), dim3(a.n), dim3(1024),
+                     0, st, a);
 }
 
 template <int K>
