@@ -1497,13 +1497,17 @@ static int g_traceback_policy = 0;
 // The streamed traceback reads each visited row whole: it wins while that
 // traffic (tiles x rows x row bytes) stays small next to what the
 // latency-bound walk costs, i.e. for the few-hundred-tile launches of the
-// LDLQ block loop.
+// LDLQ block loop. Whole encode calls measured the crossover at 192-256
+// tiles for K = 2, 3 (the bytes rule), about 384 for K = 4 (the bytes
+// rule) and between 768 and 1024 for K = 5..8, where a row is small
+// enough that the bytes rule alone would keep the streamed kernel up to
+// 3084 tiles (K = 8), 30-110 us per call too long at 1024-2048 tiles.
 static bool use_stream_traceback(const TbArgs& a) {
   if (g_traceback_policy == 1) return false;
   if (g_traceback_policy == 2) return true;
   const int64_t walk_rows = (int64_t)(a.L - 1) / exl3::row_stride(a.lay.K) + 1;
   const int64_t bytes = (int64_t)a.n * walk_rows * a.lay.row_bytes;
-  return bytes <= ((int64_t)384 << 20);
+  return bytes <= ((int64_t)384 << 20) && a.n <= 768;
 }
 
 template <int K>
