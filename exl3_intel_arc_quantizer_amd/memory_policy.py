@@ -35,7 +35,6 @@ the reserve (minus a slack for counter noise).
 
 from __future__ import annotations
 
-import dataclasses
 import os
 from dataclasses import dataclass, field
 from typing import Optional
@@ -102,6 +101,8 @@ def read_system_memory(path: str = "/proc/meminfo") -> dict:
             key, sep, rest = line.partition(":")
             if sep and key in _HOST_KEYS:
                 found[key] = int(rest.split()[0]) << 10
+                if len(found) == len(_HOST_KEYS):
+                    break  # the scratch arena snapshots once per encoder call
     return {key: found.get(key, 0) for key in _HOST_KEYS}
 
 
@@ -144,7 +145,8 @@ class MemorySnapshot:
         return self.device_free_bytes if self.gpu_available else self.system_available_bytes
 
     def as_dict(self) -> dict:
-        record = dataclasses.asdict(self)
+        # Every field is a scalar: a shallow copy is the whole record.
+        record = dict(vars(self))
         record["binding_available_bytes"] = self.binding_available_bytes
         return record
 
