@@ -154,6 +154,18 @@ class LayerQuantizationReport:
     extra: dict = field(default_factory=dict)
 
 
+def _factorization_residual_parts(H: torch.Tensor, chol: torch.Tensor,
+                                  block_rows: int = 1024) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(||H - L L^T||_F, ||H||_F) as device scalars, nothing read back."""
+    n = H.shape[0]
+    sq = torch.zeros((), dtype=torch.float64, device=H.device)
+    for i0 in range(0, n, block_rows):
+        i1 = min(n, i0 + block_rows)
+        diff = H[i0:i1] - chol[i0:i1, :i1] @ chol[:, :i1].T
+        sq += diff.square().sum(dtype=torch.float64)
+    return sq.sqrt(), torch.linalg.norm(H)
+
+
 def compute_factorization_residual(H: torch.Tensor, chol: torch.Tensor,
                                    block_rows: int = 1024) -> float:
     """||H - L L^T||_F / ||H||_F (layer_quant.py:95-101) for a lower
@@ -161,25 +173,26 @@ def compute_factorization_residual(H: torch.Tensor, chol: torch.Tensor,
     (the rows' entries past column i1 are zero), so the blocks together
     take about half the flops of the full product; each block's squared
     residual is summed in float64."""
-    n = H.shape[0]
-    sq = torch.zeros((), dtype=torch.float64, device=H.device)
-    for i0 in range(0, n, block_rows):
-        i1 = min(n, i0 + block_rows)
-        diff = H[i0:i1] - chol[i0:i1, :i1] @ chol[:, :i1].T
-        sq += diff.square().sum(dtype=torch.float64)
-    return float(sq.sqrt().item() / max(1e-12, torch.linalg.norm(H).item()))
+    res, norm = _factorization_residual_parts(H, chol, block_rows)
+    return float(res.item() / max(1e-12, norm.item()))
+
+
+def _proxy_parts(W: torch.Tensor, W_hat: torch.Tensor,
+                 H: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(tr(E^T H E), tr(W^T H W)) as float32 device scalars, E = W - W_hat."""
+    E = (W - W_hat).to(dtype=torch.float32, device=H.device)
+    H32 = H.to(torch.float32)
+    W32 = W.to(dtype=torch.float32, device=H.device)
+    return ((H32 @ E) * E).sum(), ((H32 @ W32) * W32).sum()
 
 
 def compute_proxy_loss(W: torch.Tensor, W_hat: torch.Tensor,
                        H: torch.Tensor) -> Tuple[float, float]:
     """tr(E^T H E) as sum((H E) * E), E = W - W_hat, and its ratio to
     tr(W^T H W) (layer_quant.py:104-127)."""
-    E = (W - W_hat).to(dtype=torch.float32, device=H.device)
-    H32 = H.to(torch.float32)
-    proxy = float(((H32 @ E) * E).sum().item())
-    W32 = W.to(dtype=torch.float32, device=H.device)
-    energy = max(1e-12, float(((H32 @ W32) * W32).sum().item()))
-    return proxy, proxy / energy
+    proxy_t, energy_t = _proxy_parts(W, W_hat, H)
+    proxy, energy = torch.stack([proxy_t, energy_t]).tolist()
+    return proxy, proxy / max(1e-12, energy)
 
 
 # -------------------------------------------------------------------- driver
@@ -193,7 +206,7 @@ class _PreparedModule:
     H: torch.Tensor
     reg: RegularizeResult
     ldl: BlockLDLResult
-    fact_residual: float
+    fact_parts: Tuple[torch.Tensor, torch.Tensor]  # read back with the module's metrics
     prep_seconds: float
 
 
@@ -237,16 +250,16 @@ def _prepare_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: int, cb
     key = (id(H), block_size)
     cached = ldl_cache.get(key) if ldl_cache is not None else None
     if cached is not None and cached[0] is H:
-        ldl, fact_residual = cached[1], cached[2]
+        ldl, fact_parts = cached[1], cached[2]
     else:
         H_work = H.to(torch.float32).clone()
         blockwise_preapply_had_l_(H_work, HAD_DIM)
         blockwise_preapply_had_r_(H_work, HAD_DIM)
         ldl = block_ldl(H_work, block_size=block_size)
-        fact_residual = compute_factorization_residual(H_work, ldl.cholesky)
+        fact_parts = _factorization_residual_parts(H_work, ldl.cholesky)
         if ldl_cache is not None:
-            ldl_cache[key] = (H, ldl, fact_residual)   # keeps H alive: id stays unique
-    return _PreparedModule(name=name, W=W, H=H, reg=reg, ldl=ldl, fact_residual=fact_residual,
+            ldl_cache[key] = (H, ldl, fact_parts)   # keeps H alive: id stays unique
+    return _PreparedModule(name=name, W=W, H=H, reg=reg, ldl=ldl, fact_parts=fact_parts,
                            prep_seconds=time.time() - t0)
 
 
@@ -274,14 +287,20 @@ def _finish_module(pm: _PreparedModule, lq: LDLQResult, K: int, cb: int,
     W, reg = pm.W, pm.reg
     w_hat = weight_from_quantized(lq.weight_q, reg.su, reg.sv)
     diff = W - w_hat
-    proxy, norm_proxy = compute_proxy_loss(W, w_hat, pm.H)
+    proxy_t, energy_t = _proxy_parts(W, w_hat, pm.H)
+    # Every scalar of the module comes back in one device-to-host read
+    # (float32 values widen to float64 exactly).
+    (proxy, energy, mse, diff_norm, w_norm, tile_distortion, fact_res,
+     h_norm) = torch.stack([t.to(torch.float64) for t in (
+         proxy_t, energy_t, diff.pow(2).mean(), torch.linalg.norm(diff), torch.linalg.norm(W),
+         (reg.weight - lq.weight_q).pow(2).mean(), *pm.fact_parts)]).tolist()
     metrics = ModuleMetrics(
-        mse=float(diff.pow(2).mean().item()),
-        relative_frobenius_error=float(torch.linalg.norm(diff).item()
-                                       / max(1e-12, torch.linalg.norm(W).item())),
-        tile_distortion=float((reg.weight - lq.weight_q).pow(2).mean().item()),
-        proxy_loss=proxy, normalized_proxy_loss=norm_proxy,
-        factorization_residual=pm.fact_residual, retries=pm.ldl.retries, g_scale=reg.g_scale,
+        mse=mse,
+        relative_frobenius_error=diff_norm / max(1e-12, w_norm),
+        tile_distortion=tile_distortion,
+        proxy_loss=proxy, normalized_proxy_loss=proxy / max(1e-12, energy),
+        factorization_residual=fact_res / max(1e-12, h_norm), retries=pm.ldl.retries,
+        g_scale=reg.g_scale,
         elapsed_seconds=pm.prep_seconds + shared_seconds + (time.time() - t0),
         encoder_seconds=lq.encoder_seconds, encoder_calls=lq.encoder_calls)
     return QuantizedModuleResult(name=pm.name, K=K, cb=cb, original_shape=tuple(W.shape),

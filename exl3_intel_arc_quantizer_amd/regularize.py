@@ -95,24 +95,29 @@ class RegularizeResult:
     skew_factor: Optional[float]
 
 
-def hessian_skew(H_diag: torch.Tensor) -> float:
-    """Share of sum(sqrt(diag H)) held by its largest len/50 entries."""
+def _skew_tensor(H_diag: torch.Tensor) -> torch.Tensor:
     root = torch.sort(H_diag.sqrt(), descending=True).values
     top = root.shape[0] // SKEW_FRACTION
-    return float(root[:top].sum() / root.sum())
+    return root[:top].sum() / root.sum()
+
+
+def hessian_skew(H_diag: torch.Tensor) -> float:
+    """Share of sum(sqrt(diag H)) held by its largest len/50 entries."""
+    return float(_skew_tensor(H_diag))
 
 
 def _out_scale_decision(H_diag: Optional[torch.Tensor], forced: Optional[bool],
-                        q_fallback: bool) -> Tuple[bool, Optional[float]]:
-    """(apply the output-channel scales?, skew or None). A forced value
-    wins; without one the skew decides, and without a Hessian diagonal the
-    scales apply. In fallback mode only a forced True applies them."""
+                        q_fallback: bool) -> Tuple[Optional[bool], Optional[torch.Tensor]]:
+    """(apply the output-channel scales?, skew as a device scalar or None).
+    A forced value wins; without one the skew decides, and without a
+    Hessian diagonal the scales apply. In fallback mode only a forced True
+    applies them. The decision is None when the skew makes it: the caller
+    then selects on the device and reads it back once, at the end."""
     if q_fallback:
         return bool(forced), None
     if H_diag is None:
         return (True if forced is None else bool(forced)), None
-    skew = hessian_skew(H_diag)
-    return (skew < OUT_SCALE_SKEW_CUTOFF if forced is None else bool(forced)), skew
+    return (None if forced is None else bool(forced)), _skew_tensor(H_diag)
 
 
 def _check_inputs(weight: torch.Tensor, su: torch.Tensor, sv: torch.Tensor, had_dim: int) -> None:
@@ -146,21 +151,26 @@ def regularize(weight: torch.Tensor, su: torch.Tensor, sv: torch.Tensor,
     k, n = weight.shape
     dev = weight.device
     forced = None if quant_args is None else quant_args.get("apply_out_scales")
-    apply_out, skew = _out_scale_decision(H_diag, forced, q_fallback)
+    apply_out, skew_t = _out_scale_decision(H_diag, forced, q_fallback)
     w = weight.contiguous()
 
-    # Pass 1: output-channel scales from the column RMS.
+    # Pass 1: output-channel scales from the column RMS, normalised by
+    # their mean unless W has no energy (the scales then stay as they are).
+    # Nothing is read back here: the decisions select on the device and
+    # come back together after the last pass.
     out_scales = block_rms(w, dim=0, keepdim=True)
-    mean = out_scales.mean().item()
-    zeros = not mean > _TINY
-    if zeros:
-        if forced is not None:
-            apply_out = True
-    else:
-        out_scales /= mean
+    mean = out_scales.mean()
+    live = mean > _TINY
+    out_scales /= torch.where(live, mean, torch.ones_like(mean))
+    if forced is not None and not bool(live):
+        apply_out = True          # a forced decision on an all-zero W applies the scales
     dead_cols = out_scales.abs() < _TINY
     sv = sv.to(device=dev, dtype=torch.float32).reshape(1, n).clone()
-    if apply_out:
+    if apply_out is None:
+        apply_t = skew_t < OUT_SCALE_SKEW_CUTOFF
+        out_scales.copy_(torch.where(dead_cols & apply_t, ZERO_FLOOR, out_scales))
+        sv = torch.where(apply_t, (sv * out_scales + EPS).float(), sv)
+    elif apply_out:
         out_scales[dead_cols] = ZERO_FLOOR
         sv = (sv * out_scales + EPS).float()
 
@@ -190,6 +200,14 @@ def regularize(weight: torch.Tensor, su: torch.Tensor, sv: torch.Tensor,
             raise ValueError(f"g_scale_fn returned a non-positive scale: {g_scale}")
     work *= g_scale
     su /= g_scale
+    flags = [live.to(torch.float64)]
+    if skew_t is not None:
+        flags += [skew_t.to(torch.float64), (skew_t < OUT_SCALE_SKEW_CUTOFF).to(torch.float64)]
+    flags = torch.stack(flags).tolist()          # the one read-back of the pipeline
+    zeros = not flags[0]
+    skew = flags[1] if skew_t is not None else None
+    if apply_out is None:
+        apply_out = bool(flags[2])
     if quant_args is not None:
         quant_args["zeros"] = zeros
     return RegularizeResult(apply_out_scales=bool(apply_out), weight=work, g_scale=g_scale,
