@@ -604,13 +604,17 @@ class XPUTrellisEncoder:
         end_states = idx[:, self.L - 1].astype(np.int64) & (self.edges - 1)
         results: List[EncodingResult] = []
         if build_results:
-            for i in range(n):
-                d = float(distortion[i])
-                results.append(EncodingResult(
-                    output_indices=idx[i], reconstructed=rec[i], reconstructed_perm=rec_perm[i],
-                    packed=packed[i], end_state=int(end_states[i]), distortion=d,
-                    mse=d / float(self.L),
-                    path_cost=float(path_cost[i]), K=self.K, cb=self.cb))
+            # Python scalars and per-tile row views converted in bulk (the
+            # same values and views as indexing tile by tile, at a third of
+            # the host time).
+            dists, costs, ends = distortion.tolist(), path_cost.tolist(), end_states.tolist()
+            L = float(self.L)
+            results = [EncodingResult(
+                output_indices=i_row, reconstructed=r_row, reconstructed_perm=rp_row,
+                packed=p_row, end_state=e, distortion=d, mse=d / L, path_cost=c, K=self.K,
+                cb=self.cb)
+                for i_row, r_row, rp_row, p_row, e, d, c in zip(
+                    list(idx), list(rec), list(rec_perm), list(packed), ends, dists, costs)]
         post = time.perf_counter() - t_post0 + enc["timings"].get("finalize", 0.0)
         return BatchEncodingBreakdown(
             results=results, reconstructed_tiles=rec, reconstructed_perm=rec_perm,
