@@ -15,7 +15,8 @@ distortion).
 Extra keys of the same line (each its own workload; ``--headline-only``
 skips them):
   sweep_configs2   configs[2]: 4096x4096 heavy-tailed matrix (65,536 tiles,
-                   1 % of entries x4, seed 2) at K=2..6, 8192-tile launches;
+                   1 % of entries x4, seed 2) at K=2..6 (the sweep BASELINE
+                   names) and K=1, 7, 8, 8192-tile launches;
   layer_configs3   configs[3]: LDLQ-driven 4096x4096 layer at K=4 (wall
                    time, encoder share, proxy against the committed CPU
                    pipeline fixture);
@@ -182,7 +183,7 @@ def pmc_issue(path, K):
 
 def forward_kernel_name(K):
     """The forward kernel the fast path launches for bitrate K."""
-    if 1 <= K <= 7:
+    if 1 <= K <= 8:
         return f"acs_forward_rows<K={K}>"
     return "acs_forward_generic"
 
@@ -487,12 +488,16 @@ def run_host_api(torch, tiles, K=4, steps=5):
                     ("total", bd.total_seconds))}}}
 
 
+SWEEP_K = (2, 3, 4, 5, 6, 1, 7, 8)
+
+
 def run_sweep(torch, ext, steps, profile_only=False):
-    """configs[2] at K = 2..6: whole-matrix tiles/s (8192-tile launches) and
-    the forward kernel's roofline per K."""
+    """configs[2] at K = 2..6 (and the other bitrates, 1, 7, 8):
+    whole-matrix tiles/s (8192-tile launches) and the forward kernel's
+    roofline per K."""
     big = config3_tiles()
     out = {}
-    for K in (2, 3, 4, 5, 6):
+    for K in SWEEP_K:
         b = DeviceBatch(big, K, torch, ext, batch_cap=8192)
         if profile_only:
             for _ in range(4):
@@ -529,7 +534,7 @@ def main() -> int:
                     help="with --profile-forward: the first N tiles of configs[1] only (256 is "
                          "the size of each configs[3] LDLQ call)")
     ap.add_argument("--profile-sweep", action="store_true",
-                    help="only the configs[2] forward launches (8192 tiles, K=2..6)")
+                    help="only the configs[2] forward launches (8192 tiles, K=1..8)")
     ap.add_argument("--layer", action="store_true",
                     help="only configs[3], printed as its own JSON line")
     ap.add_argument("--decoder", action="store_true",
