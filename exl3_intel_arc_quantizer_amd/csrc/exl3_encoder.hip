@@ -15,6 +15,9 @@
 //                      coalesced stores after the step's arithmetic); the
 //                      traceback recomputes the argmin of the one edge on
 //                      the path.
+//   acs_forward_chunked4 K = 4: the same step over a chunk-major, bank-
+//                      swizzled LDS layout in which a group's 16 predecessor
+//                      costs are two 16-byte loads.
 //   acs_forward_generic reference-structured kernel (one edge per thread
 //                      iteration, codebook decoded per candidate, strict fp16
 //                      '<' scan): the force_global_costs variant; writes the
@@ -136,14 +139,22 @@ __device__ __forceinline__ int lds_pos(int x) {
   return PAD ? x + (x >> KS) * PAD : x;
 }
 
+// Edge-to-LDS-position maps, passed to the shared prologue, epilogue and
+// argmin helpers: PadPos is lds_pos (edge order, optionally padded).
+template <int KS, int PAD>
+struct PadPos {
+  __device__ static __forceinline__ int at(int x) { return lds_pos<KS, PAD>(x); }
+};
+using EdgePos = PadPos<0, 0>;
+
 // Lowest-index minimum of the terminal costs (reference argmin_cost,
 // reference_encoder.py:206-214): key = cost_bits << 16 | edge; all +inf
 // gives edge 0. Result broadcast to all threads via s_red[0].
-template <int NT, int KS = 0, int PAD = 0>
+template <int NT, class Pos = EdgePos>
 __device__ uint32_t block_argmin(const uint16_t* cost, int E, uint32_t* s_red) {
   uint32_t best = 0xFFFFFFFFu;
   for (int e = threadIdx.x; e < E; e += NT)
-    best = umin(best, ((uint32_t)cost[lds_pos<KS, PAD>(e)] << 16) | (uint32_t)e);
+    best = umin(best, ((uint32_t)cost[Pos::at(e)] << 16) | (uint32_t)e);
   best = wave_min(best);
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) s_red[wave] = best;
@@ -178,7 +189,7 @@ struct FwdArgs {
 // the inputs) in the tile header, and set the initial cost vector. s_w is in
 // ring order (s_w[ri]), or with step_order in step order (s_w[i] = input
 // (i + roll) mod L).
-template <int NT, int KS = 0, int PAD = 0>
+template <int NT, class Pos = EdgePos>
 __device__ __forceinline__ void forward_prologue(const FwdArgs& a, int E, bool stash_inputs,
                                                  f16* s_w, uint16_t* cost0, int& pre_out,
                                                  bool step_order = false) {
@@ -198,21 +209,21 @@ __device__ __forceinline__ void forward_prologue(const FwdArgs& a, int E, bool s
   const int pre = a.pre_states ? a.pre_states[(int64_t)tile * a.pre_stride] : -1;
   if (threadIdx.x == 0) reinterpret_cast<int32_t*>(hdr)[exl3::HDR_PRE_STATE] = pre;
   for (int e = threadIdx.x; e < E; e += NT)
-    cost0[lds_pos<KS, PAD>(e)] = (pre < 0 || e == pre) ? 0 : 0x7C00;
+    cost0[Pos::at(e)] = (pre < 0 || e == pre) ? 0 : 0x7C00;
   pre_out = pre;
 }
 
 // Terminal costs to temp_costs and the pass-1 terminal argmin.
-template <int NT, int KS = 0, int PAD = 0>
+template <int NT, class Pos = EdgePos>
 __device__ __forceinline__ void forward_epilogue(const FwdArgs& a, int E, const uint16_t* cfin,
                                                  uint32_t* s_red) {
   const int tile = blockIdx.x;
   if (a.term_costs) {
     uint16_t* dst = a.term_costs + ((int64_t)tile * 2 + a.cost_slot) * E;
-    for (int e = threadIdx.x; e < E; e += NT) dst[e] = cfin[lds_pos<KS, PAD>(e)];
+    for (int e = threadIdx.x; e < E; e += NT) dst[e] = cfin[Pos::at(e)];
   }
   if (a.best_edges) {
-    const uint32_t b = block_argmin<NT, KS, PAD>(cfin, E, s_red);
+    const uint32_t b = block_argmin<NT, Pos>(cfin, E, s_red);
     if (threadIdx.x == 0) a.best_edges[(int64_t)tile * a.best_stride] = (int32_t)b;
   }
 }
@@ -476,7 +487,7 @@ __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forwar
         cbv[g][jp][q] = v;
       }
   int pre;
-  forward_prologue<C::NT, KS, PAD>(a, C::E, true, s_w, s_cost[0], pre, true);
+  forward_prologue<C::NT, PadPos<KS, PAD>>(a, C::E, true, s_w, s_cost[0], pre, true);
   __syncthreads();
 
   // One step; B = i & 1 is the ping-pong phase, fixed at compile time so
@@ -578,7 +589,124 @@ __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forwar
     step(Phase<0>(), i, wp.x);
     step(Phase<1>(), i + 1, wp.y);
   }
-  forward_epilogue<C::NT, KS, PAD>(a, C::E, s_cost[0], s_red);
+  forward_epilogue<C::NT, PadPos<KS, PAD>>(a, C::E, s_cost[0], s_red);
+}
+
+// ------------------------------------------------- chunk-major K = 4 kernel
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Chunk-major LDS layout of a K = 4 cost vector. Edge x = (k << 8) | h (k the
+// branch digit a group's threads compare, h the 8-bit group) sits at
+// 8 * phys(2h + (k >> 3)) + (k & 7): a group's 16 predecessor costs are two
+// 16-byte chunks. phys XORs a slot's low four bits (its place among the 16
+// chunks of a 256-byte bank row) with slot bits 5..8 (h bits 4..7); it is
+// its own inverse.
+struct ChunkPos4 {
+  __device__ static __forceinline__ int phys(int s) { return s ^ ((s >> 5) & 15); }
+  __device__ static __forceinline__ int at(int x) {
+    const int k = x >> 8, h = x & 255;
+    return phys((h << 1) | (k >> 3)) * 8 + (k & 7);
+  }
+};
+
+// K = 4 forward pass over ChunkPos4: the same arithmetic as
+// acs_forward_rows<4, ...> (80 VALU instructions per thread and step), with
+// the 16 predecessor costs of a thread's group read as two 16-byte LDS
+// loads instead of 16 two-byte ones. Wave w takes the 16 groups
+// h = (gh << 4) | w, gh = lane / 4, so each load instruction reads 16
+// chunks in 16 different places of the bank row. Lane jj = lane % 4 takes
+// the outputs x = jj + 4 (r ^ (w >> 3)), r = 0..3, packed in pairs
+// (r, r + 1): output edge (h << 4) | x sits at
+// 8 * phys((w << 5) | (x << 1) | (gh >> 3)) + (gh & 7), so output r is at
+// a per-thread base plus 128 r bytes, and each 2-byte store instruction of
+// a wave fills eight whole chunks in distinct banks. The 16-byte pieces of
+// a stored row (cost_row_pos) are whole chunks: the row gather is one LDS
+// load and one global store per piece.
+template <int CB>
+__global__ void __launch_bounds__(1024, 8) acs_forward_chunked4(FwdArgs a) {
+  constexpr int K = 4, E = 65536 >> K, NB = 1 << K, KR = 16 - K;
+  __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][E];
+  __shared__ __attribute__((aligned(4))) f16 s_w[256];
+  __shared__ uint32_t s_red[16];
+
+  const int L = a.L;
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63;
+  const int jj = lane & 3, gh = lane >> 2;
+  const int h = (gh << 4) | w;
+  const int xswap = (w >> 3) & 1;
+  const int rlo = ChunkPos4::phys(h << 1) * 8;         // k = 0..7
+  const int rhi = ChunkPos4::phys((h << 1) | 1) * 8;   // k = 8..15
+  const int wbase = ChunkPos4::at((h << K) | (jj + 4 * xswap));
+
+  // cbv[jp][k]: codebook values of branch k for the output pair
+  // (x(2 jp), x(2 jp + 1)).
+  f16x2 cbv[2][NB];
+#pragma unroll
+  for (int jp = 0; jp < 2; ++jp)
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const uint32_t s = ((uint32_t)k << KR) | ((uint32_t)h << K);
+      f16x2 v;
+      v.x = decode_state(CB, s | (uint32_t)(jj + 4 * ((2 * jp) ^ xswap)));
+      v.y = decode_state(CB, s | (uint32_t)(jj + 4 * ((2 * jp + 1) ^ xswap)));
+      cbv[jp][k] = v;
+    }
+  // Row gather: piece t (16 bytes, positions 8t .. 8t + 7 of the stored row)
+  // is the chunk of edge cost_row_edge(4, 8t).
+  constexpr int PIECES = E / 8;
+  const int gpos = tid < PIECES ? ChunkPos4::at((int)exl3::cost_row_edge(K, 8u * tid)) : 0;
+  int pre;
+  forward_prologue<1024, ChunkPos4>(a, E, true, s_w, s_cost[0], pre, true);
+  __syncthreads();
+
+  auto step = [&](auto phase, int i, f16 wv) {
+    constexpr int B = decltype(phase)::value;
+    const uint16_t* cin = s_cost[B];
+    uint16_t* cout = s_cost[B ^ 1];
+    const bool store = i >= 1 && stores_row_at<K, B>(a, i);
+    f16x2 w2;
+    w2.x = wv;
+    w2.y = wv;
+    const u32x4 c0 = *reinterpret_cast<const u32x4*>(cin + rlo);
+    const u32x4 c1 = *reinterpret_cast<const u32x4*>(cin + rhi);
+    f16x2 m[2];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const f16x2 pair = __builtin_bit_cast(f16x2, d < 4 ? c0[d & 3] : c1[d & 3]);
+      const f16x2 cv0 = __builtin_shufflevector(pair, pair, 0, 0);
+      const f16x2 cv1 = __builtin_shufflevector(pair, pair, 1, 1);
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp) {
+        const f16x2 d0 = cbv[jp][2 * d] - w2;
+        const f16x2 d1 = cbv[jp][2 * d + 1] - w2;
+        const f16x2 e0 = __builtin_elementwise_fma(d0, d0, cv0);
+        const f16x2 e1 = __builtin_elementwise_fma(d1, d1, cv1);
+        m[jp] = (d == 0) ? __builtin_elementwise_minimum(e0, e1)
+                         : __builtin_elementwise_minimum(
+                               __builtin_elementwise_minimum(m[jp], e0), e1);
+      }
+    }
+    cout[wbase] = bits_f16(m[0].x);
+    cout[wbase + 64] = bits_f16(m[0].y);
+    cout[wbase + 128] = bits_f16(m[1].x);
+    cout[wbase + 192] = bits_f16(m[1].y);
+    if (store && tid < PIECES) {
+      const RowLayout lay = exl3::make_layout(K);
+      u32x4* dst = reinterpret_cast<u32x4*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
+                                            (int64_t)exl3::cost_row_slot(lay, i - 1) *
+                                                lay.row_bytes);
+      dst[tid] = *reinterpret_cast<const u32x4*>(cin + gpos);
+    }
+    __syncthreads();
+  };
+  for (int i = 0; i < L; i += 2) {
+    const f16x2 wp = *reinterpret_cast<const f16x2*>(&s_w[i]);
+    step(Phase<0>(), i, wp.x);
+    step(Phase<1>(), i + 1, wp.y);
+  }
+  forward_epilogue<1024, ChunkPos4>(a, E, s_cost[0], s_red);
 }
 
 // --------------------------------------------------------- generic kernel
@@ -1439,6 +1567,10 @@ static void launch_fast_cb(const FwdArgs& a, hipStream_t st) {
     // More than one workgroup per CU to place: the in-place variant fits two.
     hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB, K == 1>), dim3(a.n),
                        dim3(1024), 0, st, a);
+    return;
+  }
+  if (K == 4) {
+    hipLaunchKernelGGL((acs_forward_chunked4<CB>), dim3(a.n), dim3(1024), 0, st, a);
     return;
   }
   hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB, false>), dim3(a.n), dim3(1024),
