@@ -183,9 +183,9 @@ def pmc_issue(path, K):
 
 def forward_kernel_name(K):
     """The forward kernel the fast path launches for bitrate K."""
-    if K == 4:
-        return "acs_forward_chunked4"
-    if 1 <= K <= 8:
+    if 4 <= K <= 8:
+        return f"acs_forward_chunked<K={K}>"
+    if 1 <= K <= 3:
         return f"acs_forward_rows<K={K}>"
     return "acs_forward_generic"
 

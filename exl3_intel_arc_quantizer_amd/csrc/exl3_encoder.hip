@@ -5,19 +5,19 @@
 // and its SYCL kernel FusedQuantizeKernel (quantize_kernels.sycl:245-360),
 // re-designed for CDNA4:
 //
-//   acs_forward_rows   K = 1..8. One 1024-thread workgroup per tile, fp16 path
-//                      costs ping-pong in LDS, each thread owns 64 (edge,
-//                      branch) candidates whose codebook values stay in 32
-//                      VGPRs. A step is a packed subtract and FMA per
-//                      candidate pair plus v_pk_minimum3_f16 folding two pairs
-//                      per instruction: the minimum cost per edge only. Every
+//   acs_forward_rows   K = 1..3, acs_forward_chunked K = 4..8. One
+//                      1024-thread workgroup per tile, fp16 path costs
+//                      ping-pong in LDS (edge order, or chunk-major so that
+//                      a thread's predecessor costs are 16-byte loads), each
+//                      thread owns 64 (edge, branch) candidates whose
+//                      codebook values stay in 32 VGPRs. A step is a packed
+//                      subtract and FMA per candidate pair plus
+//                      v_pk_minimum3_f16 folding two pairs per instruction:
+//                      the minimum cost per edge only. Every
 //                      row_stride(K)-th cost row goes to HBM (group-major,
 //                      coalesced stores after the step's arithmetic); the
 //                      traceback recomputes the argmin of the one edge on
 //                      the path.
-//   acs_forward_chunked4 K = 4: the same step over a chunk-major, bank-
-//                      swizzled LDS layout in which a group's 16 predecessor
-//                      costs are two 16-byte loads.
 //   acs_forward_generic reference-structured kernel (one edge per thread
 //                      iteration, codebook decoded per candidate, strict fp16
 //                      '<' scan): the force_global_costs variant; writes the
@@ -130,22 +130,13 @@ __device__ __forceinline__ uint32_t wave_min(uint32_t v) {
   return v;
 }
 
-// LDS position of edge x in a padded cost vector: PAD elements after every
-// block of 2^KS edges (KS = 16 - 2K, one block per branch k of x = (k << KS)
-// | h). The padding skews the blocks over the LDS banks, so gathering one
-// group's 2^K costs (one edge per block) is conflict-free.
-template <int KS, int PAD>
-__device__ __forceinline__ int lds_pos(int x) {
-  return PAD ? x + (x >> KS) * PAD : x;
-}
-
 // Edge-to-LDS-position maps, passed to the shared prologue, epilogue and
-// argmin helpers: PadPos is lds_pos (edge order, optionally padded).
-template <int KS, int PAD>
-struct PadPos {
-  __device__ static __forceinline__ int at(int x) { return lds_pos<KS, PAD>(x); }
+// argmin helpers: EdgePos keeps the cost vector in edge order (the generic
+// kernel and K = 1..3); ChunkMap<K> below is the chunk-major layout of
+// K = 4..8.
+struct EdgePos {
+  __device__ static __forceinline__ int at(int x) { return x; }
 };
-using EdgePos = PadPos<0, 0>;
 
 // Lowest-index minimum of the terminal costs (reference argmin_cost,
 // reference_encoder.py:206-214): key = cost_bits << 16 | edge; all +inf
@@ -234,7 +225,7 @@ __device__ __forceinline__ void forward_epilogue(const FwdArgs& a, int E, const 
 // positions 8c .. 8c + 7, gathered from LDS; the global stores stay
 // contiguous. The chunks go to the first E / 8 threads: leaving the other
 // waves free measured faster than spreading the gather over every wave.
-template <int NT, int KS = 0, int PAD = 0>
+template <int NT>
 __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const uint16_t* src,
                                                int step) {
   const RowLayout lay = exl3::make_layout(K);
@@ -247,36 +238,36 @@ __device__ __forceinline__ void store_cost_row(const FwdArgs& a, int K, const ui
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int t0 = 8 * c + 2 * m, t1 = t0 + 1;
-      const uint32_t lo = src[lds_pos<KS, PAD>(exl3::cost_row_edge(K, t0))];
-      const uint32_t hi = src[lds_pos<KS, PAD>(exl3::cost_row_edge(K, t1))];
+      const uint32_t lo = src[exl3::cost_row_edge(K, t0)];
+      const uint32_t hi = src[exl3::cost_row_edge(K, t1)];
       v[m] = lo | (hi << 16);
     }
     dst[c] = make_uint4(v[0], v[1], v[2], v[3]);
   }
 }
 
-// store_cost_row for the fast kernels, run after a step's arithmetic (the
-// stored row, the step's input, stays intact until the barrier). The row is
-// cut into pieces of W consecutive positions, the first threads taking one
-// or more pieces each; a wave's global store stays contiguous. W = 8
-// (16-byte stores) up to K = 5; at K = 6, 7, where 16-byte pieces would
-// leave the row to one or two waves, W = 2 spreads it over 4-8 waves
-// (measured: K = 6 92 -> 94 % of the VALU peak; 4-byte pieces at K = 4, 5
-// measured slower).
-template <int K, int NT, int KS, int PAD>
+// store_cost_row for the edge-order kernel (K = 1..3), run after a step's
+// arithmetic (the stored row, the step's input, stays intact until the
+// barrier): 16-byte pieces of 8 consecutive positions, the first threads
+// taking one or more each; a wave's global store stays contiguous. Each
+// step writes up to 8 KiB of rows here (2.7 TB/s at 4096 tiles): streaming
+// stores measured 80-83 -> 88 % (K = 2) and 87 -> 92-94 % (K = 3) of the
+// VALU peak.
+template <int K, int NT>
 struct RowGather {
+  static_assert(K >= 1 && K <= 3, "K = 4..8 gather from the chunk-major layout");
   static constexpr int E = 65536 >> K;
-  static constexpr int W = K >= 6 ? 2 : 8;                                   // positions per piece
-  static constexpr int PIECES = E / W;
-  static constexpr int PPT = (PIECES + NT - 1) / NT;                       // pieces per thread
-  typedef uint32_t vec __attribute__((ext_vector_type(W / 2)));
+  static constexpr int PIECES = E / 8;
+  static constexpr int PPT = (PIECES + NT - 1) / NT;  // pieces per thread
+  typedef uint32_t vec __attribute__((ext_vector_type(4)));
 
   __device__ __forceinline__ static void store(const FwdArgs& a, const uint16_t* src, int step) {
     constexpr int ks = 16 - 2 * K;
     const RowLayout lay = exl3::make_layout(K);
     vec* dst = reinterpret_cast<vec*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
                                       (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
-    if constexpr (exl3::cost_row_tree_bits(K) > 0 && PAD == 0 && W == 8) {
+    if constexpr (K > 1) {
+      static_assert(exl3::cost_row_tree_bits(K) > 0, "K = 2, 3 rows keep tree bits");
       // Positions t and t + E/2 hold the LDS neighbours x and x + 1 (x
       // even): the first E/16 threads take pieces c and c + E/16 each, from
       // eight dword reads, their halves sorted into the two pieces by
@@ -299,47 +290,26 @@ struct RowGather {
           lo[m] = __builtin_amdgcn_perm(r[2 * m + 1], r[2 * m], 0x05040100u);
           hi[m] = __builtin_amdgcn_perm(r[2 * m + 1], r[2 * m], 0x07060302u);
         }
-        if constexpr (K <= 3) {
-          __builtin_nontemporal_store(lo, &dst[c]);
-          __builtin_nontemporal_store(hi, &dst[c + HALF]);
-        } else {
-          dst[c] = lo;
-          dst[c + HALF] = hi;
-        }
+        __builtin_nontemporal_store(lo, &dst[c]);
+        __builtin_nontemporal_store(hi, &dst[c + HALF]);
       }
-      return;
-    }
+    } else {
 #pragma unroll
-    for (int j = 0; j < PPT; ++j) {
-      const int c = threadIdx.x + j * NT;
-      if (PIECES % NT == 0 || c < PIECES) {
-        vec v;
-        if constexpr (K == 1 && PAD == 0) {
+      for (int j = 0; j < PPT; ++j) {
+        const int c = threadIdx.x + j * NT;
+        if (PIECES % NT == 0 || c < PIECES) {
           // Even positions 8c + 2m from block 0, odd ones from block 1, each
           // four LDS neighbours (4c .. 4c + 3): two 8-byte reads.
           typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
           const u32x2 e = *reinterpret_cast<const u32x2*>(src + 4 * c);
           const u32x2 o = *reinterpret_cast<const u32x2*>(src + (1 << ks) + 4 * c);
+          vec v;
           v[0] = __builtin_amdgcn_perm(o.x, e.x, 0x05040100u);
           v[1] = __builtin_amdgcn_perm(o.x, e.x, 0x07060302u);
           v[2] = __builtin_amdgcn_perm(o.y, e.y, 0x05040100u);
           v[3] = __builtin_amdgcn_perm(o.y, e.y, 0x07060302u);
-        } else {
-#pragma unroll
-          for (int m = 0; m < W / 2; ++m) {
-            const int t0 = W * c + 2 * m, t1 = t0 + 1;
-            const uint32_t lo = src[lds_pos<KS, PAD>(exl3::cost_row_edge(K, t0))];
-            const uint32_t hi = src[lds_pos<KS, PAD>(exl3::cost_row_edge(K, t1))];
-            v[m] = lo | (hi << 16);
-          }
-        }
-        // K <= 3 write 8 KiB of rows per step (2.7 TB/s at 4096 tiles):
-        // streaming stores there measured 80-83 -> 88 % (K = 2) and
-        // 87 -> 92-94 % (K = 3) of the VALU peak; no difference at K >= 4.
-        if constexpr (K <= 3)
           __builtin_nontemporal_store(v, &dst[c]);
-        else
-          dst[c] = v;
+        }
       }
     }
   }
@@ -370,34 +340,34 @@ struct Phase {
 
 // ------------------------------------------------------------ fast kernels
 
-// Thread decomposition per K (exl3_layout.h keeps the same table): G groups x
-// J edges x Q branches per lane, P lanes share one edge set and split its
-// 2^K branches; 1024 threads, 64 candidates per thread and step.
+// Thread decomposition of the edge-order kernel (K = 1..3): G groups x J
+// edges x 2^K branches per thread; 1024 threads, 64 candidates per thread
+// and step.
 template <int K>
 struct FastShape {
+  static_assert(K >= 1 && K <= 3, "K = 4..8 use the chunk-major kernel");
   static constexpr int G = (K == 1) ? 16 : (K == 2 ? 4 : 1);
-  static constexpr int J = (K == 1) ? 2 : (K == 2 ? 4 : (K == 3 ? 8 : (K == 4 ? 4 : 2)));
-  static constexpr int P = (K == 6) ? 2 : (K == 7 ? 4 : (K == 8 ? 8 : 1));
+  static constexpr int J = (K == 1) ? 2 : (K == 2 ? 4 : 8);
 };
 
-template <int K, int G, int J, int P>
+template <int K, int G, int J>
 struct FastCfg {
   static constexpr int E = 65536 >> K;
   static constexpr int S = 65536 >> (2 * K);  // groups
-  static constexpr int NB = 1 << K;           // branches
-  static constexpr int Q = NB / P;            // branches per lane
-  static constexpr int NJ = NB / J;           // edge sets per group set
+  static constexpr int Q = 1 << K;            // branches
+  static constexpr int NJ = Q / J;            // edge sets per group set
   static constexpr int NGQ = S / G;           // group sets
-  static constexpr int NT = NGQ * NJ * P;     // threads per tile
+  static constexpr int NT = NGQ * NJ;         // threads per tile
   static constexpr int KR = 16 - K;
   static_assert(NT == 1024, "fast configurations use 1024 threads");
   static_assert(J % 2 == 0, "edges are processed in packed pairs (j, j + 1)");
   static_assert(G == 1 || G % 2 == 0, "groups are read in 32-bit pairs");
-  static_assert(P == 1 || P == 2 || P == 4 || P == 8, "branch split within a half row");
 };
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
+// Minimum over the P neighbouring lanes that split one output pair's
+// branches (P = 1, 2, 4, 8), left in every one of them.
 template <int P>
 __device__ __forceinline__ u16x2 group_min_u16x2(u16x2 v) {
   if (P >= 2) {
@@ -420,46 +390,36 @@ __device__ __forceinline__ u16x2 group_min_u16x2(u16x2 v) {
   return v;
 }
 
-// Cost-row forward pass (K = 1..8): minimum cost per edge, rows to HBM.
+// Edge-order forward pass (K = 1..3): minimum cost per edge, rows to HBM.
 // Thread `unit` owns edges jj*J .. jj*J + J - 1 of G groups (one group, or
-// NV runs of GV consecutive groups when G > 1), in packed pairs (j, j + 1), and the Q = 2^K / P branches k = q*P + p of
-// lane p of its P-lane group (interleaved, so the group's LDS reads fall in
-// different banks). All edges of a group share the 2^K predecessor costs, so
-// each cost is broadcast to both halves of the FMA addend (op_sel) from a
-// 16-bit LDS read (G = 1) or one half of a 32-bit read holding two groups'
-// costs (G > 1). v_pk_minimum3_f16 folds two candidates per instruction
-// into the running minimum (costs are non-negative fp16 with no NaN, where
-// IEEE minimum returns the same bits as an integer minimum). The pair minima
-// are in edge order for 32-bit LDS stores. CB is the codebook selector
-// (compile time keeps the prologue's registers low). Eight waves per SIMD:
-// two workgroups per CU, which caps VGPRs at 64. K = 1's ping-pong pair
-// of cost vectors takes 128 KiB of LDS, one workgroup per CU; INPLACE keeps
-// one vector (64 KiB) and updates it in place, with a second barrier per
-// step between the reads and the writes: two workgroups per CU, 10 % faster
-// at 1024 tiles and more, 3 % slower where one workgroup per CU is all the
-// batch fills.
-template <int K, int G, int J, int P, int CB, bool INPLACE>
+// NV runs of GV consecutive groups when G > 1), in packed pairs (j, j + 1),
+// and all 2^K branches k. All edges of a group share the 2^K predecessor
+// costs, so each cost is broadcast to both halves of the FMA addend
+// (op_sel) from a 16-bit LDS read (G = 1) or one half of a 32-bit read
+// holding two groups' costs (G > 1). v_pk_minimum3_f16 folds two candidates
+// per instruction into the running minimum (costs are non-negative fp16
+// with no NaN, where IEEE minimum returns the same bits as an integer
+// minimum). The pair minima are in edge order for 32-bit LDS stores. CB is
+// the codebook selector (compile time keeps the prologue's registers low).
+// Eight waves per SIMD: two workgroups per CU, which caps VGPRs at 64.
+// K = 1's ping-pong pair of cost vectors takes 128 KiB of LDS, one
+// workgroup per CU; INPLACE keeps one vector (64 KiB) and updates it in
+// place, with a second barrier per step between the reads and the writes:
+// two workgroups per CU, 10 % faster at 1024 tiles and more, 3 % slower
+// where one workgroup per CU is all the batch fills.
+template <int K, int G, int J, int CB, bool INPLACE>
 __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forward_rows(FwdArgs a) {
-  using C = FastCfg<K, G, J, P>;
+  using C = FastCfg<K, G, J>;
   constexpr int JP = J / 2;
-  constexpr int KS = 16 - 2 * K;
-  // One dword per branch block at K = 6, 7 (measured a loss at K <= 5). At
-  // K = 8 a block is one edge, and padding would split the pairs (e, e + 1)
-  // the outputs are stored as; its reads are conflict-free without it.
-  constexpr int PAD = (K == 6 || K == 7) ? 2 : 0;
-  constexpr int SP = C::S + PAD;                    // padded block stride
-  constexpr int EP = C::E + (1 << K) * PAD;         // padded vector length
   static_assert(C::Q % 2 == 0, "branches are folded two at a time");
-  static_assert(PAD == 0 || G == 1, "padding keeps group pairs of G > 1 together");
   static_assert(!INPLACE || K == 1, "the in-place update is written for K = 1");
-  __shared__ __attribute__((aligned(16))) uint16_t s_cost[INPLACE ? 1 : 2][EP];
+  __shared__ __attribute__((aligned(16))) uint16_t s_cost[INPLACE ? 1 : 2][C::E];
   __shared__ __attribute__((aligned(4))) f16 s_w[256];
   __shared__ uint32_t s_red[16];
 
   const int L = a.L;
   const int tid = threadIdx.x;
-  const int p = tid % P;
-  const int unit = tid / P;
+  const int unit = tid;
   const int jj = unit % C::NJ;
   // G > 1 (K = 1, 2): the thread's groups form NV runs of GV consecutive
   // groups, one 16-byte vector of pair minima each, SV groups apart; lanes
@@ -479,15 +439,15 @@ __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forwar
     for (int jp = 0; jp < JP; ++jp)
 #pragma unroll
       for (int q = 0; q < C::Q; ++q) {
-        const uint32_t s_lo = ((uint32_t)(q * P + p) << C::KR) |
-                              ((uint32_t)grp(g) << K) | (uint32_t)(jj * J + 2 * jp);
+        const uint32_t s_lo = ((uint32_t)q << C::KR) | ((uint32_t)grp(g) << K) |
+                              (uint32_t)(jj * J + 2 * jp);
         f16x2 v;
         v.x = decode_state(CB, s_lo);
         v.y = decode_state(CB, s_lo + 1u);
         cbv[g][jp][q] = v;
       }
   int pre;
-  forward_prologue<C::NT, PadPos<KS, PAD>>(a, C::E, true, s_w, s_cost[0], pre, true);
+  forward_prologue<C::NT>(a, C::E, true, s_w, s_cost[0], pre, true);
   __syncthreads();
 
   // One step; B = i & 1 is the ping-pong phase, fixed at compile time so
@@ -501,7 +461,7 @@ __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forwar
     w2.x = w;
     w2.y = w;
     if constexpr (INPLACE) {
-      static_assert(C::Q == 2 && P == 1 && JP == 1 && G % 2 == 0, "K = 1 shape");
+      static_assert(C::Q == 2 && JP == 1 && G % 2 == 0, "K = 1 shape");
       // Both predecessor costs (k = 0, 1) of every group are read, and the
       // stored row gathered, before the barrier; the new costs after it.
       uint32_t cw[2][G / 2];
@@ -509,8 +469,8 @@ __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forwar
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int g2 = 0; g2 < G / 2; ++g2)
-          cw[b][g2] = *reinterpret_cast<const uint32_t*>(cin + b * SP + grp(2 * g2));
-      if (store) RowGather<K, C::NT, KS, PAD>::store(a, cin, i - 1);
+          cw[b][g2] = *reinterpret_cast<const uint32_t*>(cin + b * C::S + grp(2 * g2));
+      if (store) RowGather<K, C::NT>::store(a, cin, i - 1);
       __syncthreads();
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -526,8 +486,7 @@ __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forwar
         const f16x2 e0 = __builtin_elementwise_fma(d0, d0, cv[0]);
         const f16x2 e1 = __builtin_elementwise_fma(d1, d1, cv[1]);
         const int e = (grp(g) << K) | (jj * J);
-        cout[lds_pos<KS, PAD>(e) >> 1] =
-            __builtin_bit_cast(uint32_t, __builtin_elementwise_minimum(e0, e1));
+        cout[e >> 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_minimum(e0, e1));
       }
       __syncthreads();
       return;
@@ -535,14 +494,13 @@ __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forwar
 
     f16x2 m[G][JP];
 #pragma unroll
-    for (int q = 0; q < C::Q; q += 2) {
-      const int k = q * P + p;
-      // cw[b][g2]: predecessor costs of branch k (b = 0) and k + P (b = 1)
+    for (int k = 0; k < C::Q; k += 2) {
+      // cw[b][g2]: predecessor costs of branch k (b = 0) and k + 1 (b = 1)
       // for groups grp(2 g2) (low half) and grp(2 g2) + 1 (high half).
       uint32_t cw[2][(G + 1) / 2];
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
-        const uint16_t* src = cin + (k + b * P) * SP;
+        const uint16_t* src = cin + (k + b) * C::S;
         if constexpr (G == 1) {
           cw[b][0] = src[grp(0)];
         } else {
@@ -562,11 +520,11 @@ __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forwar
         }
 #pragma unroll
         for (int jp = 0; jp < JP; ++jp) {
-          const f16x2 d0 = cbv[g][jp][q] - w2;
-          const f16x2 d1 = cbv[g][jp][q + 1] - w2;
+          const f16x2 d0 = cbv[g][jp][k] - w2;
+          const f16x2 d1 = cbv[g][jp][k + 1] - w2;
           const f16x2 e0 = __builtin_elementwise_fma(d0, d0, cv[0]);
           const f16x2 e1 = __builtin_elementwise_fma(d1, d1, cv[1]);
-          m[g][jp] = (q == 0) ? __builtin_elementwise_minimum(e0, e1)
+          m[g][jp] = (k == 0) ? __builtin_elementwise_minimum(e0, e1)
                               : __builtin_elementwise_minimum(
                                     __builtin_elementwise_minimum(m[g][jp], e0), e1);
         }
@@ -576,11 +534,10 @@ __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forwar
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int jp = 0; jp < JP; ++jp) {
-        const u16x2 v = group_min_u16x2<P>(__builtin_bit_cast(u16x2, m[g][jp]));
         const int e = (grp(g) << K) | (jj * J + 2 * jp);
-        if (P == 1 || p == 0) cout[lds_pos<KS, PAD>(e) >> 1] = __builtin_bit_cast(uint32_t, v);
+        cout[e >> 1] = __builtin_bit_cast(uint32_t, m[g][jp]);
       }
-    if (store) RowGather<K, C::NT, KS, PAD>::store(a, cin, i - 1);
+    if (store) RowGather<K, C::NT>::store(a, cin, i - 1);
     __syncthreads();
   };
   // L is even: steps go in pairs, whose inputs are one aligned 32-bit read.
@@ -589,76 +546,203 @@ __global__ void __launch_bounds__(1024, (K == 1 && !INPLACE ? 4 : 8)) acs_forwar
     step(Phase<0>(), i, wp.x);
     step(Phase<1>(), i + 1, wp.y);
   }
-  forward_epilogue<C::NT, PadPos<KS, PAD>>(a, C::E, s_cost[0], s_red);
+  forward_epilogue<C::NT>(a, C::E, s_cost[0], s_red);
 }
 
-// ------------------------------------------------- chunk-major K = 4 kernel
+// ------------------------------------------------ chunk-major kernels (K >= 4)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Chunk-major LDS layout of a K = 4 cost vector. Edge x = (k << 8) | h (k the
-// branch digit a group's threads compare, h the 8-bit group) sits at
-// 8 * phys(2h + (k >> 3)) + (k & 7): a group's 16 predecessor costs are two
-// 16-byte chunks. phys XORs a slot's low four bits (its place among the 16
-// chunks of a 256-byte bank row) with slot bits 5..8 (h bits 4..7); it is
-// its own inverse.
-struct ChunkPos4 {
+// Chunk-major LDS layouts of the cost vector for K = 4..8. Edge x = (k << KS)
+// | h (KS = 16 - 2K; k the branch digit a group's threads compare, h the
+// group) sits at 8 * phys((h << (K - 3)) | (k >> 3)) + (k & 7): a group's 2^K
+// predecessor costs are 2^(K-3) chunks of 16 bytes, each one LDS load. phys
+// permutes the chunk slots by XOR-ing low slot bits with higher ones (its
+// own inverse), chosen per K so that the loads, the output stores and the
+// row gather of every wave spread over the banks.
+//
+// ChunkMap<K>(tid) is thread tid's share of a step: group h, lane p of the
+// P lanes that split its 2^K branches (Q = 2^K / P each, NCH = Q / 8
+// chunks), and J outputs x(j) (edges (h << K) | x(j), packed in pairs
+// (2 jp, 2 jp + 1)). rd(c) is the LDS element offset of its c-th chunk load
+// and kof(c, m) the branch of element m of that chunk; wr(j) is the offset
+// of output j (DWORD_OUT: of the pair (x(0), x(1)), adjacent in LDS, stored
+// as one dword by lane p = 0). W is the gather's piece size in positions.
+template <int K>
+struct ChunkMap;
+
+template <>
+struct ChunkMap<4> {
+  // Wave w takes the 16 groups h = (gh << 4) | w, gh = lane / 4, so each
+  // load instruction reads 16 chunks in 16 different places of the bank
+  // row; lane jj = lane % 4 takes x = jj + 4 (j ^ (w >> 3)), whose stores
+  // are 128 bytes apart (immediate offsets) and fill eight whole chunks in
+  // distinct banks per instruction.
+  static constexpr int J = 4, P = 1, NCH = 2, W = 8;
+  static constexpr bool DWORD_OUT = false;
   __device__ static __forceinline__ int phys(int s) { return s ^ ((s >> 5) & 15); }
   __device__ static __forceinline__ int at(int x) {
-    const int k = x >> 8, h = x & 255;
-    return phys((h << 1) | (k >> 3)) * 8 + (k & 7);
+    return phys(((x & 255) << 1) | (x >> 11)) * 8 + ((x >> 8) & 7);
   }
+  int h, p, jj, xs, r0, r1, wb;
+  __device__ explicit ChunkMap(int tid) {
+    const int w = tid >> 6, lane = tid & 63;
+    jj = lane & 3;
+    h = ((lane >> 2) << 4) | w;
+    p = 0;
+    xs = (w >> 3) & 1;
+    r0 = phys(h << 1) * 8;
+    r1 = phys((h << 1) | 1) * 8;
+    wb = at((h << 4) | (jj + 4 * xs));
+  }
+  __device__ int x(int j) const { return jj + 4 * (j ^ xs); }
+  __device__ int rd(int c) const { return c ? r1 : r0; }
+  __device__ int kof(int c, int m) const { return 8 * c + m; }
+  __device__ int wr(int j) const { return wb + 64 * j; }
 };
 
-// K = 4 forward pass over ChunkPos4: the same arithmetic as
-// acs_forward_rows<4, ...> (80 VALU instructions per thread and step), with
-// the 16 predecessor costs of a thread's group read as two 16-byte LDS
-// loads instead of 16 two-byte ones. Wave w takes the 16 groups
-// h = (gh << 4) | w, gh = lane / 4, so each load instruction reads 16
-// chunks in 16 different places of the bank row. Lane jj = lane % 4 takes
-// the outputs x = jj + 4 (r ^ (w >> 3)), r = 0..3, packed in pairs
-// (r, r + 1): output edge (h << 4) | x sits at
-// 8 * phys((w << 5) | (x << 1) | (gh >> 3)) + (gh & 7), so output r is at
-// a per-thread base plus 128 r bytes, and each 2-byte store instruction of
-// a wave fills eight whole chunks in distinct banks. The 16-byte pieces of
-// a stored row (cost_row_pos) are whole chunks: the row gather is one LDS
-// load and one global store per piece.
-template <int CB>
-__global__ void __launch_bounds__(1024, 8) acs_forward_chunked4(FwdArgs a) {
-  constexpr int K = 4, E = 65536 >> K, NB = 1 << K, KR = 16 - K;
+template <>
+struct ChunkMap<5> {
+  // Wave w takes four groups (h bits 1, 2 from lane / 16, the others from
+  // w), lane jj = lane % 16 the outputs x = jj + 16 j. A group's four
+  // chunks are contiguous, in an order that depends on h & 3.
+  static constexpr int J = 2, P = 1, NCH = 4, W = 8;
+  static constexpr bool DWORD_OUT = false;
+  __device__ static __forceinline__ int phys(int s) { return s ^ ((s >> 2) & 15); }
+  __device__ static __forceinline__ int at(int x) {
+    return phys(((x & 63) << 2) | (x >> 9)) * 8 + ((x >> 6) & 7);
+  }
+  int h, p, jj, rb, w0, w1;
+  __device__ explicit ChunkMap(int tid) {
+    const int w = tid >> 6, lane = tid & 63;
+    jj = lane & 15;
+    h = (w & 1) | ((lane >> 4) << 1) | ((w >> 1) << 3);
+    p = 0;
+    rb = (phys(h << 2) & ~3) * 8;
+    w0 = at((h << 5) | jj);
+    w1 = at((h << 5) | (jj + 16));
+  }
+  __device__ int x(int j) const { return jj + 16 * j; }
+  __device__ int rd(int c) const { return rb + 8 * c; }
+  __device__ int kof(int c, int m) const { return 8 * (c ^ (h & 3)) + m; }
+  __device__ int wr(int j) const { return j ? w1 : w0; }
+};
+
+template <>
+struct ChunkMap<6> {
+  // One group per wave (h = w); lanes 2u, 2u + 1 split unit u's 64 branches
+  // (lane p loads chunks 2c + p), and unit u takes the pair x = xa, xa + 16
+  // (xa = u % 16 + 32 (u / 16)), adjacent in LDS.
+  static constexpr int J = 2, P = 2, NCH = 4, W = 2;
+  static constexpr bool DWORD_OUT = true;
+  __device__ static __forceinline__ int phys(int s) { return s ^ ((s >> 3) & 15); }
+  __device__ static __forceinline__ int at(int x) {
+    return phys(((x & 15) << 3) | (x >> 7)) * 8 + ((x >> 4) & 7);
+  }
+  int h, p, jj, xa, rb, wb;
+  __device__ explicit ChunkMap(int tid) {
+    const int w = tid >> 6, lane = tid & 63;
+    h = w;
+    p = lane & 1;
+    jj = lane >> 1;
+    xa = (jj & 15) | ((jj >> 4) << 5);
+    rb = ((phys(h << 3) & ~7) + (p ^ (h & 1))) * 8;
+    wb = at((h << 6) | xa);
+  }
+  __device__ int x(int j) const { return xa + 16 * j; }
+  __device__ int rd(int c) const { return rb + 16 * c; }
+  __device__ int kof(int c, int m) const { return 8 * (2 * (c ^ ((h >> 1) & 3)) + p) + m; }
+  __device__ int wr(int) const { return wb; }
+};
+
+template <>
+struct ChunkMap<7> {
+  // Four waves per group (h = w / 4); lanes 4u .. 4u + 3 split unit u's 128
+  // branches (lane p loads chunks 4c + p), and unit u takes the pair
+  // x = xa, xa + 4 (xa = u % 4 + 8 (u / 4)), adjacent in LDS.
+  static constexpr int J = 2, P = 4, NCH = 4, W = 2;
+  static constexpr bool DWORD_OUT = true;
+  __device__ static __forceinline__ int phys(int s) { return s ^ ((s >> 4) & 3); }
+  __device__ static __forceinline__ int at(int x) {
+    return phys(((x & 3) << 4) | (x >> 5)) * 8 + ((x >> 2) & 7);
+  }
+  int h, p, jj, xa, rb, wb;
+  __device__ explicit ChunkMap(int tid) {
+    const int w = tid >> 6, lane = tid & 63;
+    h = w >> 2;
+    p = lane & 3;
+    jj = ((w & 3) << 4) | (lane >> 2);
+    xa = (jj & 3) | ((jj >> 2) << 3);
+    rb = ((h << 4) + (p ^ h)) * 8;
+    wb = at((h << 7) | xa);
+  }
+  __device__ int x(int j) const { return xa + 4 * j; }
+  __device__ int rd(int c) const { return rb + 32 * c; }
+  __device__ int kof(int c, int m) const { return 8 * (4 * c + p) + m; }
+  __device__ int wr(int) const { return wb; }
+};
+
+template <>
+struct ChunkMap<8> {
+  // A single group in edge order; lanes 8u .. 8u + 7 split unit u's 256
+  // branches (lane p loads chunks 8c + p: eight neighbouring chunks per
+  // instruction), and unit u takes the pair x = 2u, 2u + 1.
+  static constexpr int J = 2, P = 8, NCH = 4, W = 2;
+  static constexpr bool DWORD_OUT = true;
+  __device__ static __forceinline__ int at(int x) { return x; }
+  int h, p, jj;
+  __device__ explicit ChunkMap(int tid) {
+    h = 0;
+    p = tid & 7;
+    jj = tid >> 3;
+  }
+  __device__ int x(int j) const { return 2 * jj + j; }
+  __device__ int rd(int c) const { return (8 * c + p) * 8; }
+  __device__ int kof(int c, int m) const { return 8 * (8 * c + p) + m; }
+  __device__ int wr(int) const { return 2 * jj; }
+};
+
+// Forward pass over ChunkMap<K> (K = 4..8): the arithmetic of
+// acs_forward_rows (a packed subtract and FMA per candidate pair,
+// v_pk_minimum3_f16 folding two pairs, 80 VALU instructions per thread and
+// step, plus the P-lane minimum at K >= 6), with each thread's predecessor
+// costs read as NCH 16-byte LDS loads instead of Q two-byte ones. A stored
+// row's W-position pieces (cost_row_pos) are runs of one chunk, so the row
+// gather is one LDS load and one global store per piece.
+template <int K, int CB>
+__global__ void __launch_bounds__(1024, 8) acs_forward_chunked(FwdArgs a) {
+  using M = ChunkMap<K>;
+  constexpr int E = 65536 >> K, KR = 16 - K;
+  constexpr int J = M::J, P = M::P, NCH = M::NCH, Q = 8 * NCH, JP = J / 2;
+  static_assert(Q * P == (1 << K), "the P lanes of a unit cover every branch");
   __shared__ __attribute__((aligned(16))) uint16_t s_cost[2][E];
   __shared__ __attribute__((aligned(4))) f16 s_w[256];
   __shared__ uint32_t s_red[16];
 
   const int L = a.L;
   const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63;
-  const int jj = lane & 3, gh = lane >> 2;
-  const int h = (gh << 4) | w;
-  const int xswap = (w >> 3) & 1;
-  const int rlo = ChunkPos4::phys(h << 1) * 8;         // k = 0..7
-  const int rhi = ChunkPos4::phys((h << 1) | 1) * 8;   // k = 8..15
-  const int wbase = ChunkPos4::at((h << K) | (jj + 4 * xswap));
+  const M map(tid);
 
-  // cbv[jp][k]: codebook values of branch k for the output pair
-  // (x(2 jp), x(2 jp + 1)).
-  f16x2 cbv[2][NB];
+  // cbv[jp][kk]: codebook values of branch kof(kk / 8, kk % 8) for the
+  // output pair (x(2 jp), x(2 jp + 1)).
+  f16x2 cbv[JP][Q];
 #pragma unroll
-  for (int jp = 0; jp < 2; ++jp)
+  for (int jp = 0; jp < JP; ++jp)
 #pragma unroll
-    for (int k = 0; k < NB; ++k) {
-      const uint32_t s = ((uint32_t)k << KR) | ((uint32_t)h << K);
+    for (int kk = 0; kk < Q; ++kk) {
+      const uint32_t s = ((uint32_t)map.kof(kk >> 3, kk & 7) << KR) | ((uint32_t)map.h << K);
       f16x2 v;
-      v.x = decode_state(CB, s | (uint32_t)(jj + 4 * ((2 * jp) ^ xswap)));
-      v.y = decode_state(CB, s | (uint32_t)(jj + 4 * ((2 * jp + 1) ^ xswap)));
-      cbv[jp][k] = v;
+      v.x = decode_state(CB, s | (uint32_t)map.x(2 * jp));
+      v.y = decode_state(CB, s | (uint32_t)map.x(2 * jp + 1));
+      cbv[jp][kk] = v;
     }
-  // Row gather: piece t (16 bytes, positions 8t .. 8t + 7 of the stored row)
-  // is the chunk of edge cost_row_edge(4, 8t).
-  constexpr int PIECES = E / 8;
-  const int gpos = tid < PIECES ? ChunkPos4::at((int)exl3::cost_row_edge(K, 8u * tid)) : 0;
+  // Row gather: piece t (positions W t .. W t + W - 1 of the stored row) is
+  // LDS positions at(cost_row_edge(K, W t)) onwards.
+  constexpr int W = M::W, PIECES = E / W;
+  typedef uint32_t piece_t __attribute__((ext_vector_type(W / 2)));
+  const int gpos = tid < PIECES ? M::at((int)exl3::cost_row_edge(K, (uint32_t)(W * tid))) : 0;
   int pre;
-  forward_prologue<1024, ChunkPos4>(a, E, true, s_w, s_cost[0], pre, true);
+  forward_prologue<1024, M>(a, E, true, s_w, s_cost[0], pre, true);
   __syncthreads();
 
   auto step = [&](auto phase, int i, f16 wv) {
@@ -669,35 +753,50 @@ __global__ void __launch_bounds__(1024, 8) acs_forward_chunked4(FwdArgs a) {
     f16x2 w2;
     w2.x = wv;
     w2.y = wv;
-    const u32x4 c0 = *reinterpret_cast<const u32x4*>(cin + rlo);
-    const u32x4 c1 = *reinterpret_cast<const u32x4*>(cin + rhi);
-    f16x2 m[2];
+    f16x2 m[JP];
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      const f16x2 pair = __builtin_bit_cast(f16x2, d < 4 ? c0[d & 3] : c1[d & 3]);
-      const f16x2 cv0 = __builtin_shufflevector(pair, pair, 0, 0);
-      const f16x2 cv1 = __builtin_shufflevector(pair, pair, 1, 1);
+    for (int c = 0; c < NCH; ++c) {
+      const u32x4 cw = *reinterpret_cast<const u32x4*>(cin + map.rd(c));
 #pragma unroll
-      for (int jp = 0; jp < 2; ++jp) {
-        const f16x2 d0 = cbv[jp][2 * d] - w2;
-        const f16x2 d1 = cbv[jp][2 * d + 1] - w2;
-        const f16x2 e0 = __builtin_elementwise_fma(d0, d0, cv0);
-        const f16x2 e1 = __builtin_elementwise_fma(d1, d1, cv1);
-        m[jp] = (d == 0) ? __builtin_elementwise_minimum(e0, e1)
-                         : __builtin_elementwise_minimum(
-                               __builtin_elementwise_minimum(m[jp], e0), e1);
+      for (int d = 0; d < 4; ++d) {
+        // The element goes through a named copy: __builtin_bit_cast of an
+        // ext_vector element expression compiles to a cast of element 0
+        // with this hipcc.
+        const uint32_t word = cw[d];
+        const f16x2 pair = __builtin_bit_cast(f16x2, word);
+        const f16x2 cv0 = __builtin_shufflevector(pair, pair, 0, 0);
+        const f16x2 cv1 = __builtin_shufflevector(pair, pair, 1, 1);
+        const int kk = 8 * c + 2 * d;
+#pragma unroll
+        for (int jp = 0; jp < JP; ++jp) {
+          const f16x2 d0 = cbv[jp][kk] - w2;
+          const f16x2 d1 = cbv[jp][kk + 1] - w2;
+          const f16x2 e0 = __builtin_elementwise_fma(d0, d0, cv0);
+          const f16x2 e1 = __builtin_elementwise_fma(d1, d1, cv1);
+          m[jp] = (kk == 0) ? __builtin_elementwise_minimum(e0, e1)
+                            : __builtin_elementwise_minimum(
+                                  __builtin_elementwise_minimum(m[jp], e0), e1);
+        }
       }
     }
-    cout[wbase] = bits_f16(m[0].x);
-    cout[wbase + 64] = bits_f16(m[0].y);
-    cout[wbase + 128] = bits_f16(m[1].x);
-    cout[wbase + 192] = bits_f16(m[1].y);
+    if constexpr (M::DWORD_OUT) {
+      static_assert(JP == 1, "one output pair per unit");
+      const u16x2 v = group_min_u16x2<P>(__builtin_bit_cast(u16x2, m[0]));
+      if (map.p == 0) *reinterpret_cast<uint32_t*>(cout + map.wr(0)) = __builtin_bit_cast(uint32_t, v);
+    } else {
+      static_assert(P == 1, "2-byte outputs are written by their only lane");
+#pragma unroll
+      for (int jp = 0; jp < JP; ++jp) {
+        cout[map.wr(2 * jp)] = bits_f16(m[jp].x);
+        cout[map.wr(2 * jp + 1)] = bits_f16(m[jp].y);
+      }
+    }
     if (store && tid < PIECES) {
       const RowLayout lay = exl3::make_layout(K);
-      u32x4* dst = reinterpret_cast<u32x4*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
-                                            (int64_t)exl3::cost_row_slot(lay, i - 1) *
-                                                lay.row_bytes);
-      dst[tid] = *reinterpret_cast<const u32x4*>(cin + gpos);
+      piece_t* dst = reinterpret_cast<piece_t*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
+                                                (int64_t)exl3::cost_row_slot(lay, i - 1) *
+                                                    lay.row_bytes);
+      dst[tid] = *reinterpret_cast<const piece_t*>(cin + gpos);
     }
     __syncthreads();
   };
@@ -706,7 +805,7 @@ __global__ void __launch_bounds__(1024, 8) acs_forward_chunked4(FwdArgs a) {
     step(Phase<0>(), i, wp.x);
     step(Phase<1>(), i + 1, wp.y);
   }
-  forward_epilogue<1024, ChunkPos4>(a, E, s_cost[0], s_red);
+  forward_epilogue<1024, M>(a, E, s_cost[0], s_red);
 }
 
 // --------------------------------------------------------- generic kernel
@@ -1562,19 +1661,19 @@ static int device_cus() {
 
 template <int K, int CB>
 static void launch_fast_cb(const FwdArgs& a, hipStream_t st) {
-  using Sh = FastShape<K>;
-  if (K == 1 && a.n > device_cus()) {
-    // More than one workgroup per CU to place: the in-place variant fits two.
-    hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB, K == 1>), dim3(a.n),
-                       dim3(1024), 0, st, a);
-    return;
+  if constexpr (K >= 4) {
+    hipLaunchKernelGGL((acs_forward_chunked<K, CB>), dim3(a.n), dim3(1024), 0, st, a);
+  } else {
+    using Sh = FastShape<K>;
+    if (K == 1 && a.n > device_cus()) {
+      // More than one workgroup per CU to place: the in-place variant fits two.
+      hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, CB, K == 1>), dim3(a.n), dim3(1024), 0,
+                         st, a);
+      return;
+    }
+    hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, CB, false>), dim3(a.n), dim3(1024), 0, st,
+                       a);
   }
-  if (K == 4) {
-    hipLaunchKernelGGL((acs_forward_chunked4<CB>), dim3(a.n), dim3(1024), 0, st, a);
-    return;
-  }
-  hipLaunchKernelGGL((acs_forward_rows<K, Sh::G, Sh::J, Sh::P, CB, false>), dim3(a.n), dim3(1024),
-                     0, st, a);
 }
 
 template <int K>

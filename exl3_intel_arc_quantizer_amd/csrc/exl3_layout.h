@@ -61,25 +61,9 @@ EXL3_HD constexpr inline int row_stride(int K) {
   return K == 1 ? 8 : (K == 2 ? 4 : (K <= 5 ? 2 : 1));
 }
 
-// Thread decomposition of the fast forward kernels for each K (all use 1024
-// threads and 64 candidate branches per thread per step). A thread owns J
-// edges of each of G groups, processed in packed pairs (j, j + 1); P lanes
-// split the 2^K branches of one edge set, Q = 2^K / P per lane:
-//   K : G  J  P   Q
-//   1 : 16 2  1   2
-//   2 :  4 4  1   4
-//   3 :  1 8  1   8
-//   4 :  1 4  1  16
-//   5 :  1 2  1  32
-//   6 :  1 2  2  32
-//   7 :  1 2  4  32
-//   8 :  1 2  8  32   (a single group: every edge reads all 256 costs)
-// Must match FastShape in exl3_encoder.hip.
-EXL3_HD inline int fast_G(int K) { return K == 1 ? 16 : (K == 2 ? 4 : 1); }
-EXL3_HD inline int fast_J(int K) {
-  return K == 1 ? 2 : (K == 2 ? 4 : (K == 3 ? 8 : (K == 4 ? 4 : 2)));
-}
-EXL3_HD inline int fast_P(int K) { return K == 6 ? 2 : (K == 7 ? 4 : (K == 8 ? 8 : 1)); }
+// The fast forward kernels cover K = 1..8: an edge-order kernel for K = 1..3
+// and a chunk-major one for K = 4..8 (their thread decompositions are in
+// exl3_encoder.hip). Both write the same scratch layout.
 EXL3_HD inline bool has_fast_kernel(int K) { return K >= 1 && K <= 8; }
 
 // Scratch layout of bitrate K (the same for every kernel variant, so the
