@@ -78,9 +78,23 @@ def test_configs3_layer_matches_cpu_pipeline(torch_mod):
     assert agree[-1] >= 0.99, agree[-1]
     assert agree[-8:].mean() >= 0.95, agree[-8:]
     assert agree.mean() >= 0.5, agree.mean()
-    w_rows = res.w_hat[list(fx["w_hat_row_index"])].cpu().numpy()
-    W = configs3_weight()
-    np.testing.assert_allclose(w_rows, fx["w_hat_rows"], rtol=0, atol=0.05 * np.abs(W).max())
+    # Reconstructed rows: where the encodings drifted apart, the two
+    # pipelines picked neighbouring codewords, so each row's quantisation
+    # error ||w_hat - W|| is the same within 1 % (measured within 0.15 %) and
+    # no element differs by more than half the row's RMS quantisation error
+    # (measured at most 0.27 of it).
+    idx = list(fx["w_hat_row_index"])
+    w_gpu = res.w_hat[idx].cpu().numpy().astype(np.float64)
+    w_cpu = fx["w_hat_rows"].astype(np.float64)
+    W = configs3_weight()[idx].astype(np.float64)
+    for r in range(len(idx)):
+        err_gpu = np.linalg.norm(w_gpu[r] - W[r])
+        err_cpu = np.linalg.norm(w_cpu[r] - W[r])
+        rms_cpu = err_cpu / np.sqrt(W.shape[1])
+        print(f"configs[3]: w_hat row {idx[r]}: error ratio {err_gpu / err_cpu:.4f}, "
+              f"max |diff| / RMS error {np.abs(w_gpu[r] - w_cpu[r]).max() / rms_cpu:.3f}", flush=True)
+        assert abs(err_gpu / err_cpu - 1.0) < 0.01, (idx[r], err_gpu, err_cpu)
+        assert np.abs(w_gpu[r] - w_cpu[r]).max() < 0.5 * rms_cpu, idx[r]
 
 
 def _decoder_layer(torch):
