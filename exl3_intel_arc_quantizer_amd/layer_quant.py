@@ -313,13 +313,16 @@ def quantize_linear_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: 
                            cb: int = CB_MUL1, tile_encoder: Optional[TileEncoder] = None,
                            skip_g_scale: bool = True, buf_size_k: int = DEFAULT_BUF_SIZE_K,
                            block_size: int = DEFAULT_BLOCK_SIZE,
-                           ldl_cache: Optional[dict] = None) -> QuantizedModuleResult:
+                           ldl_cache: Optional[dict] = None,
+                           time_encoder: bool = False) -> QuantizedModuleResult:
     """Quantise one linear weight with LDLQ (layer_quant.py:130-265). The
     weight is (out, in) as in ``nn.Linear`` or already (in, out) = (k, n);
     ``H`` is (in, in). Runs on the device of ``H``, which must be a GPU. The
     default encoder uses codebook ``cb``; a given encoder must match K and
     cb. ``ldl_cache`` (a dict) lets calls that pass the same Hessian tensor
-    share its factorisation."""
+    share its factorisation. ``time_encoder`` measures
+    ``metrics.encoder_seconds`` with HIP events around every encoder call,
+    which costs a 4096 x 4096 layer about 3 % (0 is reported without it)."""
     if H.device.type != "cuda":
         raise ValueError("quantize_linear_module runs on the GPU; move H to a cuda device")
     if tile_encoder is None:
@@ -328,7 +331,7 @@ def quantize_linear_module(name: str, weight: torch.Tensor, H: torch.Tensor, K: 
                          ldl_cache)
     t0 = time.time()
     lq = ldlq(weight=pm.reg.weight, L=pm.ldl.transformed, encode_tiles=tile_encoder,
-              buf_size_k=buf_size_k)
+              buf_size_k=buf_size_k, time_calls=time_encoder)
     return _finish_module(pm, lq, K, cb, time.time() - t0)
 
 
@@ -337,7 +340,8 @@ def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Ten
                            skip_g_scale: bool = True, buf_size_k: int = DEFAULT_BUF_SIZE_K,
                            block_size: int = DEFAULT_BLOCK_SIZE, memory_policy=None,
                            module_names: Optional[List[str]] = None,
-                           lockstep: bool = True) -> LayerQuantizationReport:
+                           lockstep: bool = True,
+                           time_encoder: bool = False) -> LayerQuantizationReport:
     """Quantise every bias-free ``nn.Linear`` of a decoder layer (or the
     ``module_names`` subset) with one shared encoder and scratch arena
     (layer_quant.py:268-387).
@@ -348,7 +352,8 @@ def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Ten
     q/k/v/o/gate/up of a 4096-wide layer instead of 64 to 768. The results
     equal the one-at-a-time order (``lockstep=False``, the reference's); a
     module's ``elapsed_seconds`` then includes the shared traversal and its
-    ``encoder_seconds`` is its tile share of each call."""
+    ``encoder_seconds`` is its tile share of each call. Encoder time is
+    measured only with ``time_encoder`` (HIP events around every call)."""
     from .gpu_quantizer import ScratchArena
     from .memory_policy import MemoryPolicy
 
@@ -392,7 +397,7 @@ def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Ten
             torch.cuda.synchronize(device)
             t0 = time.time()
             lqs = ldlq_lockstep([(pm.reg.weight, pm.ldl.transformed) for pm in prepared],
-                                encoder, buf_size_k=buf_size_k)
+                                encoder, buf_size_k=buf_size_k, time_calls=time_encoder)
             shared = time.time() - t0
             for pm, lq in zip(prepared, lqs):
                 results[pm.name] = _finish_module(pm, lq, K, cb, shared)
@@ -404,7 +409,7 @@ def quantize_decoder_layer(layer: torch.nn.Module, hessians: Dict[str, torch.Ten
                     name=name, weight=available[name].weight.data,
                     H=device_h[id(hessians[name])], K=K, cb=cb, tile_encoder=encoder,
                     skip_g_scale=skip_g_scale, buf_size_k=buf_size_k, block_size=block_size,
-                    ldl_cache=ldl_cache)
+                    ldl_cache=ldl_cache, time_encoder=time_encoder)
                 torch.cuda.synchronize(device)
     finally:
         arena.release()

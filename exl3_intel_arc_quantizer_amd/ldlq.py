@@ -337,7 +337,8 @@ class _Lane:
     (on a GPU with several lanes) its own stream."""
 
     def __init__(self, walks: List[_Traversal], encode_tiles: TileEncoder,
-                 synchronize: Optional[Callable[[], None]], stream=None):
+                 synchronize: Optional[Callable[[], None]], stream=None,
+                 time_calls: bool = True):
         self.walks, self.encode_tiles, self.synchronize = walks, encode_tiles, synchronize
         self.stream = stream
         schedule = lockstep_schedule([len(w.blocks) for w in walks], [w.tiles_n for w in walks])
@@ -351,7 +352,9 @@ class _Lane:
         self.fused = walks[0].on_gpu
         if self.fused:
             self.table, self.spans = _block_table(walks, self.steps)
-        self.use_events = synchronize is None and self.fused
+        # Each timing event costs the stream about 5 us (a 256-tile call is
+        # about 0.5 ms), so event timing is the caller's choice.
+        self.use_events = time_calls and synchronize is None and self.fused
         self.pending = []      # (event pair, [(walk, tiles)]) read after the loop
         self.done = 0
 
@@ -380,7 +383,8 @@ class _Lane:
             ev1 = torch.cuda.Event(enable_timing=True)
             ev1.record()
             self.pending.append(((ev0, ev1), [(walks[w], walks[w].tiles_n) for w, _ in call]))
-        else:
+        elif self.synchronize is not None or not self.fused:
+            # Host wall time: the call is synchronised, or runs on the host.
             if self.synchronize is not None:
                 self.synchronize()
             dt = time.perf_counter() - t0
@@ -451,7 +455,7 @@ def _lanes_of(walks: List[_Traversal]) -> List[List[int]]:
 
 
 def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
-                  synchronize: Optional[Callable[[], None]]) -> None:
+                  synchronize: Optional[Callable[[], None]], time_calls: bool = True) -> None:
     """Every walk's blocks through the encoder, several walks per call as
     :func:`lockstep_schedule` assigns them.
 
@@ -463,12 +467,14 @@ def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
     encoder in order, so each result is unchanged. A walk's
     ``encoder_seconds`` is its tile share of each call's duration, the
     durations scaled so that all calls together count the time during which
-    any was running."""
+    any was running; on a GPU without ``synchronize`` it is measured only
+    with ``time_calls`` (HIP events around every call) and stays 0
+    otherwise."""
     groups = _lanes_of(walks)
     concurrent = (len(groups) > 1 and walks[0].on_gpu and synchronize is None
                   and callable(getattr(encode_tiles, "fork", None)))
     if not concurrent:
-        lane = _Lane(walks, encode_tiles, synchronize)
+        lane = _Lane(walks, encode_tiles, synchronize, time_calls=time_calls)
         while lane.done < len(lane.steps):
             lane.issue()
         lane.finish()
@@ -492,7 +498,8 @@ def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
             if g:
                 stream.wait_stream(origin)
             with torch.cuda.stream(stream):
-                lanes.append(_Lane([walks[i] for i in members], enc, None, stream))
+                lanes.append(_Lane([walks[i] for i in members], enc, None, stream,
+                                   time_calls=time_calls))
         while True:
             open_lanes = [ln for ln in lanes if ln.done < len(ln.steps)]
             if not open_lanes:
@@ -522,7 +529,7 @@ def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
 
 def ldlq(weight: torch.Tensor, L: torch.Tensor, encode_tiles: TileEncoder,
          buf_size_k: int = DEFAULT_BUF_SIZE_K,
-         synchronize: Callable[[], None] = None) -> LDLQResult:
+         synchronize: Callable[[], None] = None, time_calls: bool = True) -> LDLQResult:
     """Bottom-up one-sided LDLQ (ldlq.py:163-309). ``weight`` (k, n) float32
     in the transformed basis and ``L`` (k, k) from :func:`block_ldl` are not
     modified. ``encode_tiles`` maps (tiles_n, 256) tensor-core-order tiles to
@@ -534,20 +541,22 @@ def ldlq(weight: torch.Tensor, L: torch.Tensor, encode_tiles: TileEncoder,
     strictly lower slice of L) plus the span-level feedback ``prod_cache``;
     after a span its residual is propagated into ``prod_cache``.
 
-    ``encoder_seconds`` is the encoder's share: on a CUDA weight, the sum of
-    HIP-event intervals around each call on the current stream, read once
-    after the traversal, so nothing in the loop waits for the device; with
-    ``synchronize`` given, host wall time between two ``synchronize()``
-    calls around each call instead. An encoder exposing ``check_finite``
+    ``encoder_seconds`` is the encoder's share: on a CUDA weight, with
+    ``time_calls``, the sum of HIP-event intervals around each call on the
+    current stream, read once after the traversal, so nothing in the loop
+    waits for the device (0 without ``time_calls``: the events cost the
+    stream about 5 us per call); with ``synchronize`` given, host wall time
+    between two ``synchronize()`` calls around each call instead. An encoder exposing ``check_finite``
     (the HIP adapter) is asked once at the end to raise on NaN inputs."""
     walk = _Traversal(weight, L, buf_size_k)
-    _run_lockstep([walk], encode_tiles, synchronize)
+    _run_lockstep([walk], encode_tiles, synchronize, time_calls)
     return walk.result()
 
 
 def ldlq_lockstep(problems: Sequence[Tuple[torch.Tensor, torch.Tensor]],
                   encode_tiles: TileEncoder, buf_size_k: int = DEFAULT_BUF_SIZE_K,
-                  synchronize: Callable[[], None] = None) -> List[LDLQResult]:
+                  synchronize: Callable[[], None] = None,
+                  time_calls: bool = True) -> List[LDLQResult]:
     """:func:`ldlq` on several independent (weight, L) problems at once:
     each encoder call carries the next block of several problems, as
     :func:`lockstep_schedule` balances them (as many calls as the longest
@@ -562,5 +571,5 @@ def ldlq_lockstep(problems: Sequence[Tuple[torch.Tensor, torch.Tensor]],
     devices = {w.weight.device for w in walks}
     if len(devices) != 1:
         raise ValueError(f"all problems must be on one device, got {sorted(map(str, devices))}")
-    _run_lockstep(walks, encode_tiles, synchronize)
+    _run_lockstep(walks, encode_tiles, synchronize, time_calls)
     return [w.result() for w in walks]

@@ -123,7 +123,7 @@ def test_quantize_decoder_layer_shared_arena(torch_mod):
         H, _ = hessian_from_activations(X)
         for m in members:
             hess[m] = H
-    rep = quantize_decoder_layer(layer, hess, K=3)
+    rep = quantize_decoder_layer(layer, hess, K=3, time_encoder=True)
     assert set(rep.module_results) == set(names)
     assert rep.tiles == sum(m.weight.numel() // 256 for m in layer.modules()
                             if isinstance(m, nn.Linear))
@@ -137,6 +137,8 @@ def test_quantize_decoder_layer_shared_arena(torch_mod):
         assert torch_mod.equal(r.encoded, seq.module_results[name].encoded), name
         assert torch_mod.equal(r.w_hat, seq.module_results[name].w_hat), name
         assert r.metrics.encoder_calls == k // 16 and r.metrics.encoder_seconds > 0
+        # Without time_encoder no call is timed.
+        assert seq.module_results[name].metrics.encoder_seconds == 0.0
     # One factorisation per Hessian group, equal to a module's own.
     res = rep.module_results
     assert res["self_attn.k_proj"].ldl_result is res["self_attn.q_proj"].ldl_result
@@ -213,7 +215,7 @@ def test_decoder_layer_two_lanes_equal_sequential(torch_mod):
     walks = [type("W", (), {"blocks": [0] * b, "tiles_n": t})()
              for b, t in ((16, 16), (16, 8), (16, 32), (32, 16))]
     assert ldlq_mod._lanes_of(walks) == [[3], [0, 1, 2]]
-    rep = quantize_decoder_layer(layer, hess, K=2)
+    rep = quantize_decoder_layer(layer, hess, K=2, time_encoder=True)
     seq = quantize_decoder_layer(layer, hess, K=2, lockstep=False)
     for name, r in rep.module_results.items():
         assert torch.equal(r.encoded, seq.module_results[name].encoded), name
