@@ -1125,12 +1125,9 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, ui
 #pragma unroll
     for (int u = 0; u < CH; ++u) v[c * CH + u] = q[u];
   }
-  // Every load of the tree is issued before any of it is used: a 32-byte
-  // tree (K = 5) is two dwordx4 loads, which the scheduler otherwise put on
-  // one register quad, one round trip after the other (pass-2 traceback at
-  // 4096 tiles 256 -> 211 us). Smaller trees are one load and keep the
-  // scheduler's freedom.
-  if constexpr (R * 2 > 16) __builtin_amdgcn_sched_barrier(0);
+  // A lane's leaves are at most 8 bytes (R <= 4) with every K's stride:
+  // one load per tree and lane.
+  static_assert(R <= 4, "one load of siblings per lane");
 
   uint32_t lvl[D > 0 ? D : 1][R];
 #pragma unroll
@@ -1725,20 +1722,17 @@ static FwdArgs forward_args(const float* in, int n, int K, int cb, int L, uint8_
 // (traceback_rows_kernel), 2 = streamed rows (traceback_stream_kernel).
 static int g_traceback_policy = 0;
 
-// The streamed traceback reads each visited row whole: it wins while that
-// traffic (tiles x rows x row bytes) stays small next to what the
-// latency-bound walk costs, i.e. for the few-hundred-tile launches of the
-// LDLQ block loop. Whole encode calls measured the crossover at 192-256
-// tiles for K = 2, 3 (the bytes rule), about 384 for K = 4 (the bytes
-// rule) and between 768 and 1024 for K = 5..8, where a row is small
-// enough that the bytes rule alone would keep the streamed kernel up to
-// 3084 tiles (K = 8), 30-110 us per call too long at 1024-2048 tiles.
+// The streamed traceback reads each visited row whole: per row it moves
+// tiles x row bytes at the streaming rate, where the per-row walk waits one
+// dependent tree load; the walk's row count cancels. Whole encode calls
+// measured the crossover at 128-256 tiles for K = 2, 3, about 384 for
+// K = 4, about 600 for K = 5 (each 2.5 MiB of rows per step of the walk)
+// and above 768 for K = 6..8, where the streamed kernel was 30-110 us per
+// call too long at 1024-2048 tiles.
 static bool use_stream_traceback(const TbArgs& a) {
   if (g_traceback_policy == 1) return false;
   if (g_traceback_policy == 2) return true;
-  const int64_t walk_rows = (int64_t)(a.L - 1) / exl3::row_stride(a.lay.K) + 1;
-  const int64_t bytes = (int64_t)a.n * walk_rows * a.lay.row_bytes;
-  return bytes <= ((int64_t)384 << 20) && a.n <= 768;
+  return (int64_t)a.n * a.lay.row_bytes <= ((int64_t)5 << 19) && a.n <= 768;
 }
 
 template <int K>

@@ -56,9 +56,12 @@ struct RowLayout {
 };
 
 // Steps between stored cost rows: about 8 KiB of HBM writes per step at
-// K <= 5, every step at K >= 6 (where a row is 2 KiB or less).
+// K <= 4, every step at K >= 5 (where a row is 4 KiB or less). At K = 5
+// every-step rows double the forward pass's writes but cut the traceback's
+// trees from 1024 costs to 32: a whole encode is faster at every batch size
+// (8192 tiles -2 %, 256 tiles -6 %).
 EXL3_HD constexpr inline int row_stride(int K) {
-  return K == 1 ? 8 : (K == 2 ? 4 : (K <= 5 ? 2 : 1));
+  return K == 1 ? 8 : (K == 2 ? 4 : (K <= 4 ? 2 : 1));
 }
 
 // The fast forward kernels cover K = 1..8: an edge-order kernel for K = 1..3
@@ -81,18 +84,18 @@ EXL3_HD inline RowLayout make_layout(int K) {
 EXL3_HD inline bool cost_row_stored(const RowLayout& l, int step) { return step % l.stride == 0; }
 EXL3_HD inline int cost_row_slot(const RowLayout& l, int step) { return step / l.stride; }
 // Group-major: x = (k << (16-2K)) | h at (h << K) | k, so the 2^K costs a
-// traceback step compares are one chunk. At K = 2..5, where a stored row
-// serves several steps and one traceback tree spans 2^(K * (stride + 1))
+// traceback step compares are one chunk. At K = 2..4, where a stored row
+// serves several steps and one traceback tree spans 2^(K * stride)
 // entries, the row also keeps part of the digit before k beside it: the
 // last digit (x >> (16-2K)) at positions [0, K), then the lowest
 // cost_row_tree_bits(K) bits of the digit before it, then the other bits of
-// x from bit 1 up, and x bit 0 on top. A tree then covers 16 (K = 2, 5) or
-// 4 (K = 3, 4) cache lines instead of 64, 8, 16 or 32, and positions t and
-// t + E/2 hold the neighbouring edges x and x + 1 (one dword in LDS). More
-// bits of that digit would put the forward pass's LDS gather into bank
-// conflicts.
+// x from bit 1 up, and x bit 0 on top. A tree then covers 16 (K = 2) or
+// 4 (K = 3, 4) cache lines instead of 64, 8 or 16, and positions t and
+// t + E/2 hold the neighbouring edges x and x + 1 (one dword in the
+// edge-order LDS vector of K = 2, 3). More bits of that digit would put
+// that kernel's LDS gather into bank conflicts.
 EXL3_HD constexpr inline int cost_row_tree_bits(int K) {
-  return K == 2 ? 2 : (K == 3 ? 1 : (K == 4 ? 2 : (K == 5 ? 5 : 0)));
+  return K == 2 ? 2 : (K == 3 ? 1 : (K == 4 ? 2 : 0));
 }
 EXL3_HD inline uint32_t cost_row_pos(int K, uint32_t x) {
   const int ks = 16 - 2 * K;

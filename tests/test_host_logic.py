@@ -33,7 +33,7 @@ def test_reference_formula_fixtures_still_reproducible():
 # E * 2 bytes; the header (16 bytes and 256 fp16 inputs) takes one row, two at
 # K = 8 where a row is 512 bytes.
 @pytest.mark.parametrize("k,per_tile", [(1, 33 * 65536), (2, 65 * 32768), (3, 129 * 16384),
-                                        (4, 129 * 8192), (5, 129 * 4096), (6, 256 * 2048),
+                                        (4, 129 * 8192), (5, 256 * 4096), (6, 256 * 2048),
                                         (7, 256 * 1024), (8, 257 * 512)])
 def test_layout_formula(k, per_tile):
     a = ScratchEstimator.estimate_scratch(k=k, t=256, b=10)

@@ -68,7 +68,7 @@ def test_cost_row_slots_are_a_permutation(K):
     assert lib.exl3_cost_row_slot(K, E) == -1
 
 
-@pytest.mark.parametrize("K", [1, 6, 7])
+@pytest.mark.parametrize("K", [1, 5, 6, 7])
 def test_cost_row_positions_are_group_major(K):
     """Cost rows hold predecessor edge x = (k << (16-2K)) | h at (h << K) | k."""
     lib = _native.load_library()
@@ -86,7 +86,7 @@ def _predecessors(edges, K):
     return ((k[None, :] << (16 - K)) | np.asarray(edges)[:, None]).reshape(-1) >> K
 
 
-@pytest.mark.parametrize("K,stride,run", [(2, 4, 16), (3, 2, 16), (4, 2, 64), (5, 2, 1024)])
+@pytest.mark.parametrize("K,stride,run", [(2, 4, 16), (3, 2, 16), (4, 2, 64)])
 def test_cost_rows_keep_traceback_trees_together(K, stride, run):
     """A stored row serves `stride` steps; the traceback reads, per stored
     row, the 2^(K stride) costs `stride` predecessor steps below one edge.
