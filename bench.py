@@ -89,11 +89,8 @@ def config2_tiles() -> np.ndarray:
 
 
 def config3_tiles() -> np.ndarray:
-    rng = np.random.default_rng(2)
-    W = rng.standard_normal((4096, 4096), dtype=np.float32)
-    W = np.where(rng.random(W.shape) < 0.01, 4.0 * W, W)
-    W = W.astype(np.float16).astype(np.float32)
-    return W.reshape(256, 16, 256, 16).transpose(0, 2, 1, 3).reshape(65536, 256)
+    from tests.layer_configs import configs2_tiles
+    return configs2_tiles()
 
 
 class DeviceBatch:

@@ -1,6 +1,11 @@
-"""Synthetic inputs of the two layer workloads, built
-the same way by the fixture script (tests/golden/make_layer_fixture.py, on
-the CPU), the full-size GPU tests and bench.py.
+"""Synthetic inputs of the configs[2] sweep matrix and of the two layer
+workloads, built the same way by the fixture script
+(tests/golden/make_layer_fixture.py, on the CPU), the full-size GPU tests and
+bench.py.
+
+a 4096 x 4096 N(0, 1) matrix, numpy seed 2, with a seeded 1 % of
+the entries scaled x4, rounded to fp16, cut into 65,536 tensor-core-order
+tiles (16-row blocks, ldlq.py:276-281).
 
 W ~ N(0, 0.02^2) of shape (4096 out, 4096 in), numpy seed 3;
 activations X [8192, 4096] N(0, 1), numpy seed 4, with a seeded 5 % of the
@@ -23,6 +28,15 @@ C3_W_SEED = 3
 C3_X_SEED = 4
 OUTLIER_FRACTION = 0.05
 DAMPING = 0.01
+
+
+def configs2_tiles() -> np.ndarray:
+    """The 65,536 (256-value) tiles of the configs[2] matrix."""
+    rng = np.random.default_rng(2)
+    W = rng.standard_normal((4096, 4096), dtype=np.float32)
+    W = np.where(rng.random(W.shape) < 0.01, 4.0 * W, W)
+    W = W.astype(np.float16).astype(np.float32)
+    return W.reshape(256, 16, 256, 16).transpose(0, 2, 1, 3).reshape(65536, 256)
 
 
 def synthetic_activations(rng: np.random.Generator, tokens: int, width: int,

@@ -13,6 +13,7 @@ import pytest
 from oracle import c_oracle
 from oracle.trellis_format_ref import codebook_lut as oracle_lut
 from oracle.trellis_format_ref import decode_states
+from oracle.trellis_format_ref import tensor_core_perm as oracle_tc_perm
 
 from .conftest import load_golden
 
@@ -517,6 +518,57 @@ def _path_costs(x16, idx, lut):
     return c.astype(np.float32)
 
 
+def _check_batch_invariants(x, bd, K, pre_permute, oracle_rows):
+    """Size-independent properties of an encoded batch of unit-scale tiles
+    (codebook MUL1): ring continuity and tail biting, recon == lut[idx], the
+    packing round trip on a sample, every path cost recomputed along its
+    path, every distortion recomputed in numpy's order, the upstream MSE
+    ceiling scaled by the batch's variance; ``oracle_rows`` bit-exact
+    against the C oracle."""
+    n = x.shape[0]
+    idx = bd.output_indices.astype(np.int64)
+    mask = (65536 >> K) - 1
+    np.testing.assert_array_equal(idx & mask, np.roll(idx, -1, axis=1) >> K)
+    np.testing.assert_array_equal(bd.end_states, idx[:, 255] & mask)
+    lut = oracle_lut(2)
+    np.testing.assert_array_equal(bd.reconstructed_perm.view(np.uint16), lut[idx].view(np.uint16))
+    for t in range(0, n, 1021):
+        np.testing.assert_array_equal(decode_states(bd.packed[t], K), idx[t])
+    assert np.all(np.isfinite(bd.path_costs)) and np.all(bd.path_costs > 0)
+    # The encoder sees the tiles in kernel order: permuted when pre_permute.
+    xk = x[:, oracle_tc_perm()] if pre_permute else x
+    x16 = xk.astype(np.float16)
+    np.testing.assert_array_equal(bd.path_costs, _path_costs(x16, idx, lut))
+    # Distortion over the tile in its original order (reconstructed_tiles).
+    rec = bd.reconstructed_tiles.astype(np.float32)
+    np.testing.assert_array_equal(bd.distortions, np.sum((x - rec) ** 2, axis=1))
+    mse = float(bd.distortions.mean()) / 256.0
+    var = float(x.astype(np.float64).var())
+    print(f"K={K}: {n} tiles, MSE {mse:.5f}, variance {var:.4f}, "
+          f"ceiling {MSE_CEILING[K] * var:.5f}", flush=True)
+    assert mse < MSE_CEILING[K] * var
+    ref = c_oracle.encode_tiles(x[oracle_rows], K=K, cb=2, pre_permute=pre_permute)
+    np.testing.assert_array_equal(bd.output_indices[oracle_rows], ref.output_indices)
+    np.testing.assert_array_equal(bd.path_costs[oracle_rows], ref.path_cost)
+
+
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 6])
+def test_configs2_full_matrix(K):
+    """configs[2] at its full size: the 65,536 tiles of the seed-2 heavy-tailed
+    4096 x 4096 matrix (tests/layer_configs.configs2_tiles, the matrix
+    bench.py's sweep times) at the sweep's K = 2..6, every tile checked by
+    the size-independent properties and 8 tiles bit-exact against the C
+    oracle."""
+    from .layer_configs import configs2_tiles
+    x = configs2_tiles()
+    enc = _encoder(K=K, cb=2)
+    try:
+        bd = enc.encode_batch_detailed(x, pre_permute=True, build_results=False)
+    finally:
+        enc.arena.release()
+    _check_batch_invariants(x, bd, K, True, np.arange(0, 65536, 8192) + K)
+
+
 @pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_large_batch_invariants(K):
     """Config-3-style heavy-tailed tiles at scale: size-independent properties
@@ -534,25 +586,4 @@ def test_large_batch_invariants(K):
         bd = enc.encode_batch_detailed(x, pre_permute=False, build_results=False)
     finally:
         enc.arena.release()
-    idx = bd.output_indices.astype(np.int64)
-    mask = (65536 >> K) - 1
-    np.testing.assert_array_equal(idx & mask, np.roll(idx, -1, axis=1) >> K)
-    np.testing.assert_array_equal(bd.end_states, idx[:, 255] & mask)
-    lut = oracle_lut(2)
-    np.testing.assert_array_equal(bd.reconstructed_perm.view(np.uint16), lut[idx].view(np.uint16))
-    for t in range(0, 8192, 1021):
-        np.testing.assert_array_equal(decode_states(bd.packed[t], K), idx[t])
-    assert np.all(np.isfinite(bd.path_costs)) and np.all(bd.path_costs > 0)
-    x16 = x.astype(np.float16)
-    np.testing.assert_array_equal(bd.path_costs, _path_costs(x16, idx, lut))
-    rec = bd.reconstructed_perm.astype(np.float32)
-    np.testing.assert_array_equal(bd.distortions, np.sum((x - rec) ** 2, axis=1))
-    mse = float(bd.distortions.mean()) / 256.0
-    var = float(x.astype(np.float64).var())
-    print(f"K={K}: MSE {mse:.5f}, variance {var:.4f}, ceiling {MSE_CEILING[K] * var:.5f}",
-          flush=True)
-    assert mse < MSE_CEILING[K] * var
-    sub = np.arange(0, 8192, 512)
-    ref = c_oracle.encode_tiles(x[sub], K=K, cb=2, pre_permute=False)
-    np.testing.assert_array_equal(bd.output_indices[sub], ref.output_indices)
-    np.testing.assert_array_equal(bd.path_costs[sub], ref.path_cost)
+    _check_batch_invariants(x, bd, K, False, np.arange(0, 8192, 512))
