@@ -32,25 +32,41 @@ step). It is bound by fp16 VALU issue: one wave64 VALU instruction per CU
 per cycle, 256 CUs, 2.4 GHz peak engine clock; a packed-fp16 FMA slot is
 64 lanes x 2 halves x 2 FLOP = 256 FLOP, so the VALU peak is the published
 157.3 TFLOP/s fp16 vector rate.
-  roofline.achieved  VALU instructions per launch (SQ_INSTS_VALU from the
-                     committed rocprofv3 counters, scaled to the launch's
-                     tiles) x 256 FLOP / the launch duration measured live
-                     with HIP events on the launch stream;
-  roofline.frac      achieved / 157.3 = VALU issue utilisation at the
-                     nominal clock; it cannot exceed 1;
+  roofline.achieved  the algorithm's FLOP per launch / the launch duration
+                     measured live with HIP events on the launch stream:
+                     4 FLOP per trellis candidate (fp16 subtract, FMA = 2,
+                     compare-select), 256 x 65,536 candidates per tile and
+                     pass (the reference's work unit,
+                     scripts/benchmark_phase1_encoder.py:57-60);
+  roofline.frac      achieved / 157.3;
+  roofline.isa_ceiling
+                     0.8: on gfx950 a candidate costs at least 1.25 issue
+                     slots (packed subtract and FMA per two candidates, a
+                     v_pk_minimum3_f16 per four), so frac cannot exceed
+                     4 / (1.25 x 4);
+  roofline.issue_frac
+                     VALU instructions actually issued per launch
+                     (SQ_INSTS_VALU from the committed rocprofv3 counters,
+                     scaled to the launch's tiles) x 256 FLOP / the live
+                     duration / 157.3: instruction issue at the nominal
+                     clock, overhead instructions included. Null unless the
+                     counter row names the same kernel and the same encoder
+                     source (sha256 prefix) as this run;
   roofline.issue_at_measured_clock
                      SQ_INSTS_VALU / (256 CUs x GRBM_GUI_ACTIVE / 8) of the
-                     committed counter run: utilisation at the clock the GPU
-                     actually ran (about 2.2 GHz under this load);
-  roofline.algorithmic
-                     4 FLOP per trellis candidate (fp16 subtract, FMA = 2,
-                     compare-select) / duration / 157.3. On gfx950 a
-                     candidate costs at least 1.25 issue slots (packed
-                     subtract and FMA, a quarter of a v_pk_minimum3_f16),
-                     so this view tops out at 4 / (1.25 x 4) = 0.8;
+                     committed counter run: issue at the clock the GPU ran;
+  roofline.lds       the algorithm's LDS bytes (2^(26-K) per tile and pass:
+                     every step reads and writes the E fp16 costs) / the
+                     duration against 128 B per CU and clock (78.6 TB/s),
+                     and the measured LDS-busy share of CU cycles
+                     (SQ_LDS_IDX_ACTIVE) from the committed counters;
   step_frac          the whole step's algorithmic FLOP / ms_per_step / 157.3.
 traffic: HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE
 counters (copy-kernel calibration), null when the summary has no row.
+
+cpu_baseline (beside the headline, k2 and every sweep K): the C restatement
+of the reference encoder on the GPU box's host cores, timed on a bounded
+sample of the same matrix before anything touches the GPU.
 
     python bench.py [--steps 10] [--warmup 2] [--headline-only] [--no-cpu-baseline]
     python bench.py --profile-forward --k-list 4,2   # forward launches only
@@ -80,6 +96,22 @@ FLOP_PER_VALU_SLOT = 64 * 2 * 2                 # lanes x packed halves x FMA
 FLOP_PER_CANDIDATE = 4                          # subtract, FMA (2), compare-select
 CANDIDATES_PER_TILE_PASS = 256 * 65536
 ISA_CEILING = FLOP_PER_CANDIDATE / (1.25 * FLOP_PER_VALU_SLOT / 64)   # = 0.8
+LDS_BYTES_PER_CU_CLOCK = 128
+PEAK_LDS_TBPS = CUS * LDS_BYTES_PER_CU_CLOCK * NOMINAL_CLOCK_HZ / 1e12    # 78.6
+ENCODER_SOURCES = ("exl3_intel_arc_quantizer_amd/csrc/exl3_encoder.hip",
+                   "exl3_intel_arc_quantizer_amd/csrc/exl3_layout.h")
+
+
+def encoder_source_sha() -> str:
+    """First 12 hex digits of the sha256 of the encoder's kernel sources:
+    committed counter rows carry it, and a row measured on other sources is
+    not used."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in ENCODER_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:12]
 
 
 def config2_tiles() -> np.ndarray:
@@ -168,22 +200,32 @@ def pmc_traffic(path, K, tiles):
     return None
 
 
-def pmc_issue(path, K):
-    """Counters of the forward launch at bitrate K from the committed PMC
-    summary, rows ``| issue | K | tiles | SQ_INSTS_VALU | GRBM_GUI_ACTIVE |
-    duration us |`` (per dispatch); None if absent."""
-    for k, t, valu, grbm, us in (r[:5] for r in summary_rows(path, "issue")):
-        if int(k) == K:
-            return {"tiles": int(t), "valu": float(valu), "grbm": float(grbm), "us": float(us)}
+def pmc_row(path, tag, K, kernel, source, fields):
+    """The ``| tag | K | tiles | <fields...> | kernel | source |`` row of a
+    committed PMC summary for bitrate K, as floats keyed by ``fields`` plus
+    ``tiles``; None if absent or measured on another kernel or source."""
+    for cells in summary_rows(path, tag):
+        if int(cells[0]) != K or len(cells) < len(fields) + 4:
+            continue
+        row_kernel, row_source = cells[len(fields) + 2], cells[len(fields) + 3]
+        if row_kernel.strip("`") != kernel or row_source.strip("`") != source:
+            return None
+        out = {"tiles": int(cells[1])}
+        out.update({f: float(v) for f, v in zip(fields, cells[2:2 + len(fields)])})
+        return out
     return None
 
 
-def forward_kernel_name(K):
-    """The forward kernel the fast path launches for bitrate K."""
+def forward_kernel_name(K, tiles=4096, cus=CUS, cb=2):
+    """The forward kernel instance the fast path launches for bitrate K and
+    a launch of ``tiles`` tiles (rocprofv3's name without the argument
+    list)."""
     if 4 <= K <= 8:
-        return f"acs_forward_chunked<K={K}>"
+        return f"acs_forward_chunked<{K}, {cb}>"
     if 1 <= K <= 3:
-        return f"acs_forward_rows<K={K}>"
+        g, j = {1: (16, 2), 2: (4, 4), 3: (1, 8)}[K]
+        inplace = "true" if K == 1 and tiles > cus else "false"
+        return f"acs_forward_rows<{K}, {g}, {j}, {cb}, {inplace}>"
     return "acs_forward_generic"
 
 
@@ -206,29 +248,39 @@ def time_forward(batch, torch, reps=3):
 
 def valu_roofline(K, tiles, launch_s, summary):
     """The forward kernel under the fp16 VALU roofline (see the module
-    docstring): issue utilisation from the committed counters and the live
-    launch duration, with the algorithmic-FLOP view beside it."""
-    alg_tflops = tiles * CANDIDATES_PER_TILE_PASS * FLOP_PER_CANDIDATE / launch_s / 1e12
-    out = {"bound": "valu", "achieved": None, "peak": PEAK_FP16_VECTOR_TFLOPS,
-           "unit": "TFLOP/s", "frac": None, "traffic": pmc_traffic(summary, K, tiles),
-           "kernel": forward_kernel_name(K), "launch_ms": round(launch_s * 1e3, 4),
-           "tiles_per_launch": tiles,
-           "algorithmic": {"tflops": round(alg_tflops, 2),
-                           "frac": round(alg_tflops / PEAK_FP16_VECTOR_TFLOPS, 4),
-                           "isa_ceiling": ISA_CEILING,
-                           "of_isa_ceiling": round(alg_tflops / PEAK_FP16_VECTOR_TFLOPS
-                                                   / ISA_CEILING, 4)},
-           "counters": os.path.relpath(summary, ROOT)}
-    c = pmc_issue(summary, K)
+    docstring): the algorithm's FLOP rate from the live launch duration,
+    with the issued-instruction view and the LDS figures beside it."""
+    kernel = forward_kernel_name(K, tiles)
+    source = encoder_source_sha()
+    alg = tiles * CANDIDATES_PER_TILE_PASS * FLOP_PER_CANDIDATE / launch_s / 1e12
+    frac = alg / PEAK_FP16_VECTOR_TFLOPS
+    lds_bytes = tiles * (1 << (26 - K))
+    out = {"bound": "valu", "achieved": round(alg, 2), "peak": PEAK_FP16_VECTOR_TFLOPS,
+           "unit": "TFLOP/s", "frac": round(frac, 4), "isa_ceiling": ISA_CEILING,
+           "of_isa_ceiling": round(frac / ISA_CEILING, 4),
+           "traffic": pmc_traffic(summary, K, tiles), "kernel": kernel,
+           "launch_ms": round(launch_s * 1e3, 4), "tiles_per_launch": tiles,
+           "work": "4 FLOP per trellis candidate, 256 x 65536 candidates per tile and pass",
+           "issue_frac": None,
+           "lds": {"algorithmic_bytes_per_launch": lds_bytes,
+                   "achieved_tbps": round(lds_bytes / launch_s / 1e12, 2),
+                   "peak_tbps": round(PEAK_LDS_TBPS, 1),
+                   "frac": round(lds_bytes / launch_s / 1e12 / PEAK_LDS_TBPS, 4),
+                   "busy_measured": None},
+           "counters": os.path.relpath(summary, ROOT), "source_sha": source}
+    c = pmc_row(summary, "issue", K, kernel, source,
+                ("valu", "grbm", "us"))
     if c is not None:
         instr = c["valu"] * tiles / c["tiles"]                 # wave64 VALU instructions
-        achieved = instr * FLOP_PER_VALU_SLOT / launch_s / 1e12
+        issued = instr * FLOP_PER_VALU_SLOT / launch_s / 1e12
         clock = c["grbm"] / 8.0 / (c["us"] * 1e-6)             # GRBM_GUI_ACTIVE sums 8 XCDs
-        out.update(achieved=round(achieved, 2),
-                   frac=round(achieved / PEAK_FP16_VECTOR_TFLOPS, 4),
+        out.update(issue_frac=round(issued / PEAK_FP16_VECTOR_TFLOPS, 4),
                    valu_instructions_per_launch=int(round(instr)),
                    issue_at_measured_clock=round(c["valu"] / (CUS * c["grbm"] / 8.0), 4),
                    measured_clock_ghz=round(clock / 1e9, 3))
+    d = pmc_row(summary, "lds", K, kernel, source, ("lds_active", "grbm", "us"))
+    if d is not None:
+        out["lds"]["busy_measured"] = round(d["lds_active"] / (CUS * d["grbm"] / 8.0), 4)
     return out
 
 
@@ -262,19 +314,20 @@ def cpu_baseline_numpy(tiles, K, cores):
                       "restatement of reference_encoder.py, one process per core)"}
 
 
-def cpu_baseline(tiles, K):
+def cpu_baseline(tiles, K, per_core=16, what="the benchmark matrix"):
     """The C oracle (oracle/libexl3_oracle.so, a port of the reference's CPU
-    encoder) on a bounded sample of the same workload, all host cores."""
+    encoder) on a bounded sample of the same workload: ``per_core`` tiles
+    per host core, all cores (OpenMP over tiles)."""
     from oracle import c_oracle
     cores = c_oracle.default_threads()
-    n = 16 * cores                                   # ~10 s of CPU work
+    n = min(per_core * cores, tiles.shape[0])
     sample = tiles[:n]
     c_oracle.encode_tiles(sample[:1], K=K, cb=2, pre_permute=True, threads=1)  # load + warm
     t0 = time.perf_counter()
     c_oracle.encode_tiles(sample, K=K, cb=2, pre_permute=True, threads=cores)
     dt = time.perf_counter() - t0
     return {"value": round(n / dt, 3), "unit": "tiles/s", "cores": cores, "kind": "port",
-            "sample": f"first {n} tiles of the benchmark matrix at K={K} "
+            "sample": f"first {n} tiles of {what} at K={K} "
                       f"({dt:.1f} s, C restatement of reference_encoder.py, OpenMP)"}
 
 
@@ -442,38 +495,73 @@ def run_decoder_config(torch, K=4, cpu_tiles_per_s=None, lockstep=True, gss=Fals
 REFERENCE_API_TILES_PER_S = 1711.51     # artifacts/benchmarks/encoder_b580.json (Arc B580)
 
 
+def reference_round_trip_adapter(encoder):
+    """An LDLQ tile encoder with the reference adapter's per-call work
+    (exl3_quant/ldlq.py:370-380): tiles copied to a host numpy array, the
+    host-array ``encode_batch`` (EncodingResult records), the records'
+    reconstructions and states stacked, and both copied back to the tiles'
+    device. The product adapter keeps the tiles on the device instead."""
+    import torch
+
+    def encode(tiles):
+        arr = np.ascontiguousarray(tiles.detach().cpu().numpy(), dtype=np.float32)
+        results = encoder.encode_batch(arr, pre_permute=False)
+        rec = np.stack([r.reconstructed for r in results]).astype(np.float32)
+        idx = np.stack([r.output_indices for r in results]).astype(np.uint16)
+        return (torch.from_numpy(rec).to(tiles.device),
+                torch.from_numpy(idx.view(np.int16)).to(tiles.device))
+    return encode
+
+
+def _median_call_seconds(fn, arg, torch, calls=3):
+    times = []
+    for _ in range(calls):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn(arg)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[calls // 2], times
+
+
 def run_host_api(torch, tiles, K=4, steps=5):
-    """Two API-level rates with the host in the loop.
+    """API-level rates with the host in the loop.
 
     * ``reference_method``: the reference's own benchmark
-      (scripts/measure_encoder.py:39-56): make_xpu_tile_encoder(K=2), a
-      1024-tile warm-up call, then one timed call on 65,536 tiles of
-      torch.randn(., 256) x 0.02 (seed 42) on the device, wall clock between
-      device synchronisations. The reference published 1,711.51 tiles/s for
-      it on an Arc B580. Its adapter copied tiles to the host and back per
-      call; this one keeps them on the device.
+      (scripts/measure_encoder.py:39-56): an adapter at K=2, a 1024-tile
+      warm-up call, then calls on 65,536 tiles of torch.randn(., 256) x 0.02
+      (seed 42) on the device, wall clock between device synchronisations,
+      the median of 3 calls. The reference published 1,711.51 tiles/s for
+      it on an Arc B580 (artifacts/benchmarks/encoder_b580.json), through
+      an adapter that copies every call's tiles to numpy and back and builds
+      an EncodingResult per tile (ldlq.py:370-380).
+      ``numpy_round_trip`` times that same per-call work over this encoder
+      (the like-for-like comparison); ``device_resident`` times the product
+      adapter (make_xpu_tile_encoder), which keeps tiles and results in HBM.
     * ``host_array``: configs[1] through encode_batch_detailed
       (xpu_quantizer.py:707-909) with numpy in and out, EncodingResult
       records included, so PCIe transfers and host assembly are inside the
       timing (median of ``steps`` calls)."""
     from exl3_intel_arc_quantizer_amd.gpu_quantizer import XPUTrellisEncoder
     from exl3_intel_arc_quantizer_amd.tile_encoder import make_xpu_tile_encoder
+    torch.manual_seed(42)
+    t65 = torch.randn(65536, 256, device="cuda") * 0.02
+    warm = torch.randn(1024, 256, device="cuda") * 0.02
+    torch.cuda.synchronize()
+    rates = {}
     enc2 = make_xpu_tile_encoder(K=2, asynchronous=False)
     try:
-        warm = torch.randn(1024, 256, device="cuda") * 0.02
         enc2(warm)
-        torch.cuda.synchronize()
-        del warm
-        torch.manual_seed(42)
-        t65 = torch.randn(65536, 256, device="cuda") * 0.02
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        enc2(t65)
-        torch.cuda.synchronize()
-        ref_dt = time.perf_counter() - t0
-        del t65
+        med, each = _median_call_seconds(enc2, t65, torch)
+        rates["device_resident"] = (med, each)
+        host_enc = XPUTrellisEncoder(K=2, cb=2, arena=enc2.encoder.arena)
+        round_trip = reference_round_trip_adapter(host_enc)
+        round_trip(warm)
+        med, each = _median_call_seconds(round_trip, t65, torch)
+        rates["numpy_round_trip"] = (med, each)
     finally:
         enc2.encoder.arena.release()
+    del t65, warm
     enc = XPUTrellisEncoder(K=K, cb=2)
     try:
         enc.encode_batch_detailed(tiles, pre_permute=True)
@@ -485,16 +573,21 @@ def run_host_api(torch, tiles, K=4, steps=5):
         dt = sorted(times)[steps // 2]
     finally:
         enc.arena.release()
+    ref = {name: {"value": round(65536 / med, 1), "unit": "tiles/s",
+                  "seconds_median": round(med, 4),
+                  "seconds_each": [round(t, 4) for t in each]}
+           for name, (med, each) in rates.items()}
+    like = ref["numpy_round_trip"]["value"]
     return {"reference_method": {
-                "value": round(65536 / ref_dt, 1), "unit": "tiles/s", "K": 2, "tiles": 65536,
-                "seconds": round(ref_dt, 4),
+                "K": 2, "tiles": 65536, "calls_timed": 3, **ref,
                 "reference_published_arc_b580": REFERENCE_API_TILES_PER_S,
-                "ratio_to_reference_published": round(65536 / ref_dt
-                                                      / REFERENCE_API_TILES_PER_S, 1)},
+                "ratio_to_reference_published": round(like / REFERENCE_API_TILES_PER_S, 1),
+                "ratio_basis": "numpy_round_trip (the reference adapter's per-call work)"},
             "host_array": {
                 "value": round(tiles.shape[0] / dt, 1), "unit": "tiles/s", "K": K,
                 "workload": "configs[1]", "tiles": int(tiles.shape[0]),
                 "ms_per_call": round(dt * 1e3, 3),
+                "note": "PCIe-inclusive: numpy in, numpy and EncodingResult records out",
                 "breakdown_ms": {k: round(v * 1e3, 3) for k, v in (
                     ("transfer", bd.transfer_seconds), ("search", bd.search_seconds),
                     ("traceback", bd.traceback_seconds), ("post_process", bd.postprocess_seconds),
@@ -504,10 +597,22 @@ def run_host_api(torch, tiles, K=4, steps=5):
 SWEEP_K = (2, 3, 4, 5, 6, 1, 7, 8)
 
 
-def run_sweep(torch, ext, steps, profile_only=False):
+def sweep_cpu_baselines(per_core=4):
+    """The C oracle's rate per sweep K on the first ``per_core`` tiles per
+    host core of the configs[2] matrix (run before the GPU is touched)."""
+    big = config3_tiles()
+    out = {}
+    for K in SWEEP_K:
+        out[K] = cpu_baseline(big, K, per_core=per_core, what="the configs[2] matrix")
+        print(f"# CPU baseline configs[2] K={K}: {out[K]['value']} tiles/s", file=sys.stderr,
+              flush=True)
+    return out
+
+
+def run_sweep(torch, ext, steps, profile_only=False, cpu=None):
     """configs[2] at K = 2..6 (and the other bitrates, 1, 7, 8):
     whole-matrix tiles/s (8192-tile launches) and the forward kernel's
-    roofline per K."""
+    roofline per K, with the C oracle's rate per K from ``cpu``."""
     big = config3_tiles()
     out = {}
     for K in SWEEP_K:
@@ -521,9 +626,10 @@ def run_sweep(torch, ext, steps, profile_only=False):
             launch_s, n = time_forward(b, torch, reps=2)
             rf = valu_roofline(K, n, launch_s, PMC_CONFIGS2)
             out[K] = {"tiles_per_s": round(big.shape[0] / sec, 1),
-                      "ms_per_matrix": round(sec * 1e3, 3), "roofline": rf}
+                      "ms_per_matrix": round(sec * 1e3, 3), "roofline": rf,
+                      "cpu_baseline": (cpu or {}).get(K)}
             print(f"# sweep K={K}: {big.shape[0] / sec:,.0f} tiles/s, forward "
-                  f"{rf['launch_ms']} ms / 8192 tiles, VALU issue {rf['frac']}", file=sys.stderr,
+                  f"{rf['launch_ms']} ms / 8192 tiles, roofline frac {rf['frac']}", file=sys.stderr,
                   flush=True)
         del b
         torch.cuda.empty_cache()
@@ -574,6 +680,7 @@ def main() -> int:
     only = args.layer or args.decoder or args.host_api
     profiling = args.profile_forward or args.profile_sweep
     cpu = cpu_np = None
+    cpu_k, cpu_sweep = {}, None
     if not args.no_cpu_baseline and not profiling and not (only and not args.decoder):
         # Host baselines first: nothing has touched the GPU yet.
         cpu = cpu_baseline(tiles, head)
@@ -582,6 +689,12 @@ def main() -> int:
             print(f"# CPU baselines at K={head}: C {cpu['value']} tiles/s, numpy "
                   f"{cpu_np['value']} tiles/s on {cpu['cores']} cores", file=sys.stderr,
                   flush=True)
+            for K in k_list[1:]:
+                cpu_k[K] = cpu_baseline(tiles, K, per_core=4)
+                print(f"# CPU baseline at K={K}: C {cpu_k[K]['value']} tiles/s",
+                      file=sys.stderr, flush=True)
+            if not args.headline_only:
+                cpu_sweep = sweep_cpu_baselines()
 
     import torch
 
@@ -635,7 +748,8 @@ def main() -> int:
         results[K] = {"tiles_per_s": b.n / sec, "ms_per_step": sec * 1e3, "roofline": rf,
                       "step_frac": round(step_flop / sec / 1e12 / PEAK_FP16_VECTOR_TFLOPS, 4)}
         print(f"# K={K}: {b.n / sec:,.0f} tiles/s, {sec * 1e3:.2f} ms/step, forward "
-              f"{rf['launch_ms']} ms, VALU issue {rf['frac']} (nominal clock), "
+              f"{rf['launch_ms']} ms, roofline frac {rf['frac']} (isa ceiling {ISA_CEILING}), "
+              f"issue {rf['issue_frac']} (nominal clock), "
               f"{rf.get('issue_at_measured_clock')} (measured clock)", file=sys.stderr,
               flush=True)
         del b
@@ -666,10 +780,11 @@ def main() -> int:
     for K in k_list[1:]:
         line[f"k{K}"] = {"value": round(results[K]["tiles_per_s"], 1), "unit": "tiles/s",
                          "ms_per_step": round(results[K]["ms_per_step"], 3),
-                         "roofline": results[K]["roofline"], "step_frac": results[K]["step_frac"]}
+                         "roofline": results[K]["roofline"], "step_frac": results[K]["step_frac"],
+                         "cpu_baseline": cpu_k.get(K)}
     if not args.headline_only:
         t0 = time.perf_counter()
-        line["sweep_configs2"] = run_sweep(torch, ext, max(1, args.steps // 5))
+        line["sweep_configs2"] = run_sweep(torch, ext, max(1, args.steps // 5), cpu=cpu_sweep)
         line["layer_configs3"] = run_layer_config(torch)
         print(f"# configs[3]: {line['layer_configs3']['value']} s", file=sys.stderr, flush=True)
         line["decoder_configs4"] = run_decoder_config(

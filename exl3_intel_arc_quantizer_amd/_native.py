@@ -34,6 +34,8 @@ _SIGNATURES = {
     "exl3_cost_row_slot": (_c_i64, [_c_int, _c_i64]),
     "exl3_quantize_tiles": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int,
                                      _c_int, _c_int, _c_int, _c_i64, _c_vp]),
+    "exl3_quantize_tiles_tb": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
+                                        _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_vp]),
     "exl3_quantize_tiles_noalloc": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
                                              _c_int, _c_vp]),
     "exl3_forward_pass": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
@@ -91,13 +93,24 @@ def load_library(path: Optional[Path] = None):
 TRACEBACK_POLICIES = {"auto": 0, "rows": 1, "stream": 2}
 
 
-def set_traceback_policy(policy: str) -> str:
-    """Choose the traceback kernel for later calls in this process: "auto"
-    (by batch size), "rows" (per-row tree loads) or "stream" (whole rows
-    streamed through LDS); results are identical. Returns the previous one."""
+def _policy_code(policy: Optional[str]) -> int:
+    """C-ABI code of a traceback policy name; None = the process default (-1)."""
+    if policy is None:
+        return -1
     if policy not in TRACEBACK_POLICIES:
         raise ValueError(f"policy must be one of {sorted(TRACEBACK_POLICIES)}, got {policy!r}")
-    prev = load_library().exl3_set_traceback_policy(TRACEBACK_POLICIES[policy])
+    return TRACEBACK_POLICIES[policy]
+
+
+def set_traceback_policy(policy: str) -> str:
+    """Choose the default traceback kernel for later calls in this process
+    that do not name one: "auto" (by batch size), "rows" (per-row tree
+    loads) or "stream" (whole rows streamed through LDS); results are
+    identical. Returns the previous default. ``quantize_tiles(...,
+    traceback_policy=...)`` chooses per call without changing it."""
+    if policy is None:
+        raise ValueError("set_traceback_policy needs a policy name")
+    prev = load_library().exl3_set_traceback_policy(_policy_code(policy))
     return {v: k for k, v in TRACEBACK_POLICIES.items()}[prev]
 
 def last_error() -> str:
@@ -223,9 +236,14 @@ class QuantizeExtension:
     # quantize_xpu.cpp:112-167
     def quantize_tiles(self, input_tiles, output_tiles, output_indices, temp_costs, temp_edges,
                        K: int, mcg: bool, mul1: bool, sg_size: int = 32,
-                       force_global_costs: bool = False, wave_cap_override: int = 0) -> None:
+                       force_global_costs: bool = False, wave_cap_override: int = 0,
+                       traceback_policy: Optional[str] = None) -> None:
+        """The reference's arguments, plus ``traceback_policy`` (no counterpart
+        there): the traceback kernel for this call only, "auto", "rows",
+        "stream", or None for the process default."""
         torch = _torch()
         cb = _resolve_cb(mcg, mul1)
+        tb = _policy_code(traceback_policy)
         dev = _check_device_tensor(input_tiles, "input_tiles", torch.float32, 2)
         if _check_device_tensor(output_tiles, "output_tiles", torch.float32, 2) != dev:
             raise RuntimeError("output_tiles must be on the same GPU device as input_tiles")
@@ -241,10 +259,10 @@ class QuantizeExtension:
         if tuple(output_indices.shape) != (n, L):
             raise RuntimeError("output_indices shape must match input_tiles")
         with torch.cuda.device(dev):
-            _check(self.lib.exl3_quantize_tiles(
+            _check(self.lib.exl3_quantize_tiles_tb(
                 input_tiles.data_ptr(), output_tiles.data_ptr(), output_indices.data_ptr(),
                 temp_costs.data_ptr(), temp_edges.data_ptr(), batch_cap, n, K, cb, L,
-                int(bool(force_global_costs)), int(wave_cap_override), _stream(dev)),
+                int(bool(force_global_costs)), int(wave_cap_override), tb, _stream(dev)),
                 "quantize_tiles")
 
     # quantize_xpu.cpp:169-215

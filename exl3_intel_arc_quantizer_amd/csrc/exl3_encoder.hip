@@ -53,6 +53,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -1720,7 +1721,14 @@ static FwdArgs forward_args(const float* in, int n, int K, int cb, int L, uint8_
 
 // Traceback kernel choice: 0 = by batch size, 1 = per-row tree loads
 // (traceback_rows_kernel), 2 = streamed rows (traceback_stream_kernel).
-static int g_traceback_policy = 0;
+// The process default (exl3_set_traceback_policy) applies to calls that do
+// not name one; exl3_quantize_tiles_tb takes the choice per call, so two
+// threads or streams can choose differently without touching the default.
+static std::atomic<int> g_traceback_policy{0};
+
+static int resolve_policy(int policy) {
+  return policy < 0 ? g_traceback_policy.load(std::memory_order_relaxed) : policy;
+}
 
 // The streamed traceback reads each visited row whole: per row it moves
 // tiles x row bytes at the streaming rate, where the per-row walk waits one
@@ -1729,15 +1737,15 @@ static int g_traceback_policy = 0;
 // K = 4, about 600 for K = 5 (each 2.5 MiB of rows per step of the walk)
 // and above 768 for K = 6..8, where the streamed kernel was 30-110 us per
 // call too long at 1024-2048 tiles.
-static bool use_stream_traceback(const TbArgs& a) {
-  if (g_traceback_policy == 1) return false;
-  if (g_traceback_policy == 2) return true;
+static bool use_stream_traceback(const TbArgs& a, int policy) {
+  if (policy == 1) return false;
+  if (policy == 2) return true;
   return (int64_t)a.n * a.lay.row_bytes <= ((int64_t)5 << 19) && a.n <= 768;
 }
 
 template <int K>
-static void launch_traceback_rows(const TbArgs& a, hipStream_t st) {
-  if (use_stream_traceback(a)) {
+static void launch_traceback_rows(const TbArgs& a, int policy, hipStream_t st) {
+  if (use_stream_traceback(a, policy)) {
     const dim3 blk(StreamShape<K>::THREADS);
     switch (a.cb) {
       case 0: hipLaunchKernelGGL((traceback_stream_kernel<K, 0>), dim3(a.n), blk, 0, st, a); break;
@@ -1753,17 +1761,19 @@ static void launch_traceback_rows(const TbArgs& a, hipStream_t st) {
   }
 }
 
-static int launch_traceback(const TbArgs& a, hipStream_t st) {
+// policy: 0..2 as above, -1 = the process default.
+static int launch_traceback(const TbArgs& a, int policy, hipStream_t st) {
   if (a.n <= 0) return 0;
+  const int p = resolve_policy(policy);
   switch (a.lay.K) {
-    case 1: launch_traceback_rows<1>(a, st); break;
-    case 2: launch_traceback_rows<2>(a, st); break;
-    case 3: launch_traceback_rows<3>(a, st); break;
-    case 4: launch_traceback_rows<4>(a, st); break;
-    case 5: launch_traceback_rows<5>(a, st); break;
-    case 6: launch_traceback_rows<6>(a, st); break;
-    case 7: launch_traceback_rows<7>(a, st); break;
-    default: launch_traceback_rows<8>(a, st); break;
+    case 1: launch_traceback_rows<1>(a, p, st); break;
+    case 2: launch_traceback_rows<2>(a, p, st); break;
+    case 3: launch_traceback_rows<3>(a, p, st); break;
+    case 4: launch_traceback_rows<4>(a, p, st); break;
+    case 5: launch_traceback_rows<5>(a, p, st); break;
+    case 6: launch_traceback_rows<6>(a, p, st); break;
+    case 7: launch_traceback_rows<7>(a, p, st); break;
+    default: launch_traceback_rows<8>(a, p, st); break;
   }
   return check_launch("traceback");
 }
@@ -1793,9 +1803,7 @@ const char* exl3_version(void) { return EXL3_VERSION; }
 int exl3_set_traceback_policy(int policy) {
   if (policy < 0 || policy > 2)
     return set_error("traceback policy must be 0, 1 or 2, got %d", policy), -1;
-  const int previous = g_traceback_policy;
-  g_traceback_policy = policy;
-  return previous;
+  return g_traceback_policy.exchange(policy);
 }
 
 int exl3_decode_codebook(int cb, uint16_t* lut, void* stream) {
@@ -1860,13 +1868,16 @@ int exl3_backward_pass(const uint16_t* temp_costs, const uint8_t* temp_edges, fl
     t.out_w = out_w;
     t.out_idx = out_idx;
   }
-  return launch_traceback(t, st);
+  return launch_traceback(t, -1, st);
 }
 
-int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_t* temp_costs,
-                        uint8_t* temp_edges, int64_t batch_cap, int64_t n, int K, int cb, int L,
-                        int generic, int64_t wave_cap, void* stream) {
+int exl3_quantize_tiles_tb(const float* in, float* out_w, int16_t* out_idx,
+                           uint16_t* temp_costs, uint8_t* temp_edges, int64_t batch_cap,
+                           int64_t n, int K, int cb, int L, int generic, int64_t wave_cap,
+                           int traceback, void* stream) {
   if (validate_common(K, cb, L)) return 1;
+  if (traceback < -1 || traceback > 2)
+    return set_error("traceback must be -1, 0, 1 or 2, got %d", traceback);
   if (n <= 0) return set_error("num_tiles must be positive, got %lld", (long long)n);
   if (batch_cap < 1) return set_error("temp_costs batch dimension B must be >= 1");
   if (!in || !out_w || !out_idx || !temp_costs || !temp_edges) return set_error("NULL buffer");
@@ -1898,7 +1909,7 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
     t1.start_stride = hstride;
     t1.end_out = end_states;
     t1.end_stride = hstride;
-    if (launch_traceback(t1, st)) return 1;
+    if (launch_traceback(t1, traceback, st)) return 1;
     // Pass 2: natural order, wrap constrained to the end state (:290-293).
     a.roll = 0;
     a.store_from = 0;
@@ -1912,9 +1923,16 @@ int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_
     t2.start_stride = hstride;
     t2.out_w = out_w + off * L;
     t2.out_idx = out_idx + off * L;
-    if (launch_traceback(t2, st)) return 1;
+    if (launch_traceback(t2, traceback, st)) return 1;
   }
   return 0;
+}
+
+int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_t* temp_costs,
+                        uint8_t* temp_edges, int64_t batch_cap, int64_t n, int K, int cb, int L,
+                        int generic, int64_t wave_cap, void* stream) {
+  return exl3_quantize_tiles_tb(in, out_w, out_idx, temp_costs, temp_edges, batch_cap, n, K, cb,
+                                L, generic, wave_cap, -1, stream);
 }
 
 int exl3_quantize_tiles_noalloc(const float* in, float* out_w, int16_t* out_idx, int64_t n,

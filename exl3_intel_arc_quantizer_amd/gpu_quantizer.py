@@ -112,7 +112,8 @@ def verify_tile_encoding_quality(result: EncodingResult, reference: EncodingResu
 
 @dataclass
 class ScratchArenaLogEntry:
-    """One arena action with its memory context (xpu_quantizer.py:172-185)."""
+    """One arena action with its memory context (the reference's record,
+    xpu_quantizer.py:172-185)."""
 
     action: str                     # "allocate", "reuse", "evict", "retry-shrink", "release"
     k: int
@@ -126,20 +127,86 @@ class ScratchArenaLogEntry:
     snapshot: dict
 
 
+def _halvings(b: int):
+    """Candidate batch sizes b, b // 2, ..., 1."""
+    while b > 1:
+        yield b
+        b //= 2
+    yield 1
+
+
+@dataclass(frozen=True)
+class _Refusal:
+    """Why one candidate batch was not admitted, as plain data: no
+    exception, traceback or tensor outlives the attempt."""
+
+    message: str
+    need_bytes: int
+    usable_bytes: int
+    snapshot: object
+    context: str
+    from_policy: bool
+
+
+@dataclass
+class _Slot:
+    """The arena's resident scratch: one device byte buffer holding the
+    terminal costs (B, 2, E) fp16 followed by B tiles of cost rows."""
+
+    key: Tuple[int, int, int, int]          # (device, K, L, B)
+    storage: object
+    temp_costs: object
+    temp_edges: object
+
+    @classmethod
+    def carve(cls, key, storage, est) -> "_Slot":
+        import torch
+
+        _, k, tile_len, b = key
+        split = est.costs_bytes                 # b * 4E: a multiple of 1 KiB
+        costs = storage[:split].view(torch.float16).view(b, 2, est.states)
+        edges = storage[split:].view(b, tile_rows(k, tile_len), scratch_row_bytes(k))
+        return cls(key, storage, costs, edges)
+
+    @property
+    def nbytes(self) -> int:
+        return int(self.storage.numel())
+
+    def serves(self, device: int, k: int, tile_len: int, b: int) -> bool:
+        return self.key[:3] == (device, k, tile_len) and self.key[3] >= b
+
+
 class ScratchArena:
-    """Bounded single-slot scratch arena for ``temp_costs``/``temp_edges``
-    (xpu_quantizer.py:188-506): at most one buffer pair is resident; a change
-    of (device, K, L) or a larger request synchronises the stream and releases
-    it; a failed admission or allocation halves B down to 1."""
+    """Scratch for ``temp_costs`` / ``temp_edges`` with at most one resident
+    slot (the contract of xpu_quantizer.py:188-506).
+
+    * ``acquire`` returns ``(temp_costs, temp_edges, admitted_b)``. A slot of
+      the same (device, K, L) with at least the requested batch is handed
+      back; any other resident slot is evicted first, so at most one is ever
+      held.
+    * A slot is ONE device allocation, costs first, then the cost rows (sizes
+      from ``ScratchEstimator``), so an admission asks the memory policy
+      about a single figure and its single-allocation ceiling bounds the
+      slot.
+    * Candidate batches run from the request down to 1, halving. A candidate
+      the policy refuses, or whose allocation, hook or post-commit check
+      fails, is dropped (its buffer freed and the allocator's cache
+      trimmed) before the next is tried. When even one tile is refused the
+      call raises ``MemoryPressureError``, built from plain data so that
+      holding it keeps no frame, buffer or earlier exception alive.
+    * Reuse is stream-ordered when ``synchronize_reuse=False``: device-
+      resident callers that launch everything on one stream need no host
+      synchronisation to recycle the slot. The host-array API synchronises.
+    * ``history`` records every action with its memory context; the counters
+      count reuses, evictions, allocations and halvings.
+    """
 
     def __init__(self, policy: Optional[MemoryPolicy] = None, device_index: int = 0,
                  default_cap_b: int = 4096):
         self.policy = policy or MemoryPolicy()
         self.device_index = device_index
         self.default_cap_b = default_cap_b
-        self._key: Optional[Tuple[int, int, int, int]] = None
-        self._temp_costs = None
-        self._temp_edges = None
+        self._slot: Optional[_Slot] = None
         self.history: List[ScratchArenaLogEntry] = []
         self.high_water_scratch_bytes = 0
         self.evictions = 0
@@ -148,160 +215,153 @@ class ScratchArena:
         self.retries = 0
 
     @property
-    def current_key(self):
-        return self._key
+    def current_key(self) -> Optional[Tuple[int, int, int, int]]:
+        return None if self._slot is None else self._slot.key
 
     @property
     def resident_bytes(self) -> int:
-        if self._temp_costs is None or self._temp_edges is None:
-            return 0
-        return int(self._temp_costs.numel() * self._temp_costs.element_size()
-                   + self._temp_edges.numel() * self._temp_edges.element_size())
+        return 0 if self._slot is None else self._slot.nbytes
 
-    def _log(self, action, k, t, req, adm, scratch, staging, out_bytes, usable, snap):
+    # ------------------------------------------------------------ helpers
+
+    def _target(self, requested_b: Optional[int]) -> int:
+        b = self.default_cap_b if requested_b is None else int(requested_b)
+        if b < 1:
+            raise ValueError(f"requested_b must be >= 1, got {b}")
+        return b
+
+    def _budget(self, staging: int):
+        """Snapshot, bytes the process holds beyond this arena's slot plus
+        host staging, and the policy's admissible bytes given those."""
+        snap = capture_snapshot(self.device_index)
+        outstanding = max(0, snap.device_allocated_bytes - self.resident_bytes) + staging
+        return snap, outstanding, self.policy.usable_bytes(snap, outstanding_bytes=outstanding)
+
+    def _note(self, action: str, k: int, tile_len: int, requested: int, admitted: int,
+              nbytes: int, staging: int, snap, usable: int) -> None:
         self.history.append(ScratchArenaLogEntry(
-            action=action, k=k, tile_len=t, requested_b=req, admitted_b=adm,
-            scratch_bytes=scratch, distinct_staging_bytes=staging,
-            outstanding_xpu_bytes=out_bytes, usable_budget_bytes=usable,
+            action=action, k=k, tile_len=tile_len, requested_b=requested, admitted_b=admitted,
+            scratch_bytes=nbytes, distinct_staging_bytes=staging,
+            outstanding_xpu_bytes=snap.device_allocated_bytes, usable_budget_bytes=usable,
             snapshot=snap.as_dict()))
+
+    def _drop(self, action: str) -> None:
+        """Free the resident slot after the device has finished with it."""
+        import torch
+
+        slot, self._slot = self._slot, None
+        if slot is None:
+            return
+        _, k, tile_len, b = slot.key
+        torch.cuda.synchronize(self.device_index)
+        del slot
+        torch.cuda.empty_cache()
+        snap, _, usable = self._budget(0)
+        self._note(action, k, tile_len, b, 0, 0, 0, snap, usable)
+
+    def _commit(self, k: int, tile_len: int, b: int, staging: int,
+                hook: Optional[Callable[[int], None]]):
+        """Try one candidate batch: a new ``_Slot`` or a ``_Refusal``."""
+        import torch
+
+        est = ScratchEstimator.estimate_scratch(k=k, b=b, t=tile_len)
+        snap, outstanding, usable = self._budget(staging)
+        storage = None
+        try:
+            self.policy.check(est.total_bytes, snap, outstanding_bytes=outstanding,
+                              context=f"K={k} B={b} scratch admit")
+            if hook is not None:
+                hook(b)
+            storage = torch.empty(est.total_bytes, dtype=torch.uint8,
+                                  device=f"cuda:{self.device_index}")
+            self.policy.check_after_commit(capture_snapshot(self.device_index),
+                                           pre_snapshot=snap, expected_bytes=est.total_bytes,
+                                           context=f"K={k} B={b} post-commit")
+        except MemoryPressureError as exc:
+            refusal = _Refusal(str(exc), exc.need_bytes, exc.usable_bytes, exc.snapshot,
+                               exc.context, True)
+        except Exception as exc:  # noqa: BLE001 - allocator or hook failure: try a smaller B
+            refusal = _Refusal(f"{type(exc).__name__}: {exc}", est.total_bytes, usable, snap,
+                               f"K={k} B={b} allocation", False)
+        else:
+            slot = _Slot.carve((self.device_index, k, tile_len, b), storage, est)
+            self.allocations += 1
+            self.high_water_scratch_bytes = max(self.high_water_scratch_bytes, slot.nbytes)
+            after, _, left = self._budget(staging)
+            self._note("allocate", k, tile_len, b, b, slot.nbytes, staging, after, left)
+            return slot
+        if storage is not None:
+            storage = None
+            torch.cuda.empty_cache()
+        return refusal
+
+    # ------------------------------------------------------------ contract
 
     def adaptive_batch_capacity(self, k: int, tile_len: int = 256,
                                 requested_b: Optional[int] = None,
                                 distinct_staging_bytes: int = 0) -> int:
-        """Largest admissible B (xpu_quantizer.py:234-269)."""
-        import torch
-
-        target_b = requested_b if requested_b is not None else self.default_cap_b
-        if target_b < 1:
-            raise ValueError(f"requested_b must be >= 1, got {target_b}")
-        snap = capture_snapshot(self.device_index)
-        outstanding = max(0, int(torch.cuda.memory_allocated(self.device_index))
-                          - self.resident_bytes) + distinct_staging_bytes
-        usable = self.policy.usable_bytes(snap, outstanding_bytes=outstanding)
-        per_b = ScratchEstimator.estimate_scratch(k=k, b=1, t=tile_len)
-        max_by_budget = usable // per_b.total_bytes
+        """Largest batch, at most the request, whose slot the policy would
+        admit now (the reference's P1-11 query, xpu_quantizer.py:234-269).
+        Raises ``MemoryPressureError`` when not even one tile fits."""
+        target = self._target(requested_b)
+        per_tile = ScratchEstimator.estimate_scratch(k=k, b=1, t=tile_len).total_bytes
+        snap, outstanding, usable = self._budget(distinct_staging_bytes)
+        room = usable
         if self.policy.max_single_alloc_bytes is not None:
-            max_by_budget = min(max_by_budget,
-                                self.policy.max_single_alloc_bytes // max(1, per_b.edges_bytes))
-        if max_by_budget < 1:
-            self.policy.check(per_b.total_bytes, snap, outstanding_bytes=outstanding,
+            room = min(room, self.policy.max_single_alloc_bytes)
+        if room < per_tile:
+            self.policy.check(per_tile, snap, outstanding_bytes=outstanding,
                               context=f"adaptive_batch_capacity K={k} B=1")
-        return int(max(1, min(target_b, max_by_budget)))
+        return max(1, min(target, room // per_tile))
 
     def release(self) -> None:
-        import torch
-
-        if self._temp_costs is None and self._temp_edges is None:
-            return
-        torch.cuda.synchronize(self.device_index)
-        k, t, b = (self._key[1], self._key[2], self._key[3]) if self._key else (0, 0, 0)
-        self._temp_costs = None
-        self._temp_edges = None
-        self._key = None
-        torch.cuda.empty_cache()
-        snap = capture_snapshot(self.device_index)
-        out_bytes = int(torch.cuda.memory_allocated(self.device_index))
-        self._log("release", k, t, b, 0, 0, 0, out_bytes,
-                  self.policy.usable_bytes(snap, out_bytes), snap)
+        """Synchronise the device and free the resident slot, if any."""
+        self._drop("release")
 
     def acquire(self, k: int, tile_len: int = 256, requested_b: Optional[int] = None,
                 distinct_staging_bytes: int = 0,
                 allocator_hook: Optional[Callable[[int], None]] = None,
                 synchronize_reuse: bool = True):
-        """Return ``(temp_costs, temp_edges, admitted_b)`` (xpu_quantizer.py:313-506).
-        ``synchronize_reuse=False`` hands a resident buffer back without the
-        device synchronisation: correct when every user of the buffers
-        launches on one HIP stream, whose order already serialises them."""
+        """``(temp_costs, temp_edges, admitted_b)`` for ``requested_b`` tiles
+        (default ``default_cap_b``) of bitrate ``k`` and length ``tile_len``.
+        ``allocator_hook(b)`` runs before each allocation attempt; an
+        exception from it counts as an allocation failure at that b.
+        ``distinct_staging_bytes`` (host memory the caller will hold beside
+        the scratch) is charged against the budget."""
         import torch
 
-        target_b = requested_b if requested_b is not None else self.default_cap_b
-        if target_b < 1:
-            raise ValueError(f"requested_b must be >= 1, got {target_b}")
-
-        if (self._key is not None and self._key[0] == self.device_index and self._key[1] == k
-                and self._key[2] == tile_len and self._key[3] >= target_b
-                and self._temp_costs is not None and self._temp_edges is not None):
+        target = self._target(requested_b)
+        slot = self._slot
+        if slot is not None and slot.serves(self.device_index, k, tile_len, target):
             if synchronize_reuse:
                 torch.cuda.synchronize(self.device_index)
             self.reuses += 1
-            snap = capture_snapshot(self.device_index)
-            out_bytes = snap.device_allocated_bytes
-            self._log("reuse", k, tile_len, target_b, target_b, self.resident_bytes,
-                      distinct_staging_bytes, out_bytes,
-                      self.policy.usable_bytes(snap, out_bytes + distinct_staging_bytes), snap)
-            return self._temp_costs[:target_b], self._temp_edges[:target_b], target_b
-
-        if self._temp_costs is not None or self._temp_edges is not None:
+            snap, _, usable = self._budget(distinct_staging_bytes)
+            self._note("reuse", k, tile_len, target, target, slot.nbytes,
+                       distinct_staging_bytes, snap, usable)
+            return slot.temp_costs[:target], slot.temp_edges[:target], target
+        if slot is not None:
+            del slot
             self.evictions += 1
-            self.release()
+            self._drop("evict")
 
-        cand_b = target_b
-        last_err: Optional[Exception] = None
-        rb = scratch_row_bytes(k)
-        while cand_b >= 1:
-            est = ScratchEstimator.estimate_scratch(k=k, b=cand_b, t=tile_len)
-            snap = capture_snapshot(self.device_index)
-            out_bytes = int(torch.cuda.memory_allocated(self.device_index))
-            effective_outstanding = out_bytes + distinct_staging_bytes
-            costs = edges = None
-            try:
-                self.policy.check(max(est.costs_bytes, est.edges_bytes), snap,
-                                  outstanding_bytes=effective_outstanding,
-                                  context=f"K={k} B={cand_b} single-buffer ceiling")
-                usable = self.policy.usable_bytes(snap, outstanding_bytes=effective_outstanding)
-                if est.total_bytes > usable:
-                    raise MemoryPressureError(
-                        f"memory-pressure abort [K={k} B={cand_b} scratch admit]: "
-                        f"need {est.total_bytes} B > usable {usable} B",
-                        est.total_bytes, usable, snap, f"K={k} B={cand_b} scratch admit")
-                if allocator_hook is not None:
-                    allocator_hook(cand_b)
-                dev = f"cuda:{self.device_index}"
-                costs = torch.empty((cand_b, 2, est.states), dtype=torch.float16, device=dev)
-                edges = torch.empty((cand_b, tile_rows(k, tile_len), rb), dtype=torch.uint8,
-                                    device=dev)
-                post = capture_snapshot(self.device_index)
-                self.policy.check_after_commit(post, pre_snapshot=snap,
-                                               expected_bytes=est.total_bytes,
-                                               context=f"K={k} B={cand_b} post-commit")
-                self._key = (self.device_index, k, tile_len, cand_b)
-                self._temp_costs, self._temp_edges = costs, edges
-                self.allocations += 1
-                self.high_water_scratch_bytes = max(self.high_water_scratch_bytes,
-                                                    est.total_bytes)
-                self._log("allocate", k, tile_len, target_b, cand_b, est.total_bytes,
-                          distinct_staging_bytes,
-                          int(torch.cuda.memory_allocated(self.device_index)), usable, post)
-                return costs, edges, cand_b
-            except Exception as exc:  # noqa: BLE001 - any failure shrinks B
-                if costs is not None or edges is not None:
-                    del costs, edges
-                    costs = edges = None
-                    torch.cuda.empty_cache()
-                last_err = exc
-                if cand_b == 1:
-                    break
-                next_b = max(1, cand_b // 2)
+        refusal: Optional[_Refusal] = None
+        for b in _halvings(target):
+            outcome = self._commit(k, tile_len, b, distinct_staging_bytes, allocator_hook)
+            if isinstance(outcome, _Slot):
+                self._slot = outcome
+                return outcome.temp_costs, outcome.temp_edges, b
+            refusal = outcome
+            if b > 1:
                 self.retries += 1
-                self._log("retry-shrink", k, tile_len, cand_b, next_b, est.total_bytes,
-                          distinct_staging_bytes, out_bytes,
-                          self.policy.usable_bytes(snap, effective_outstanding), snap)
-                cand_b = next_b
-
-        if isinstance(last_err, MemoryPressureError):
-            clean = MemoryPressureError(str(last_err), last_err.need_bytes,
-                                        last_err.usable_bytes, last_err.snapshot,
-                                        last_err.context)
-        else:
-            snap = capture_snapshot(self.device_index)
-            out_bytes = int(torch.cuda.memory_allocated(self.device_index))
-            clean = MemoryPressureError(
-                f"scratch allocation failed even at B=1 for K={k}: {last_err}",
-                ScratchEstimator.estimate_scratch(k=k, b=1, t=tile_len).total_bytes,
-                self.policy.usable_bytes(snap, out_bytes + distinct_staging_bytes), snap,
-                context=f"K={k} B=1 minimum batch failure")
-        del last_err
-        raise clean from None
+                self._note("retry-shrink", k, tile_len, b, b // 2,
+                           ScratchEstimator.estimate_scratch(k=k, b=b, t=tile_len).total_bytes,
+                           distinct_staging_bytes, refusal.snapshot, refusal.usable_bytes)
+        reason = refusal.message if refusal.from_policy else (
+            f"no scratch for K={k}, L={tile_len}: every batch from {target} down to 1 tile "
+            f"failed; at B=1: {refusal.message}")
+        raise MemoryPressureError(reason, refusal.need_bytes, refusal.usable_bytes,
+                                  refusal.snapshot, refusal.context) from None
 
 
 @dataclass
@@ -430,7 +490,7 @@ class XPUTrellisEncoder:
             raise ValueError(f"Unknown traceback_mode {mode!r}")
 
     def _run_chunks(self, ext, x_dev, out_w, out_i, temp_costs, temp_edges, admitted_b, mode,
-                    timings, synchronize=True):
+                    timings, synchronize=True, traceback_policy=None):
         """Encode x_dev (n, L) kernel-order tiles chunk by chunk."""
         import torch
 
@@ -441,7 +501,8 @@ class XPUTrellisEncoder:
             ts = time.perf_counter()
             ext.quantize_tiles(x_dev, out_w, out_i, temp_costs[:admitted_b],
                                temp_edges[:admitted_b], self.K, self.mcg_flag, self.mul1_flag,
-                               self.sg_size, self.force_global_costs, self.wave_cap_override)
+                               self.sg_size, self.force_global_costs, self.wave_cap_override,
+                               traceback_policy=traceback_policy)
             if synchronize:
                 torch.cuda.synchronize(self.device_index)
                 timings["search"] += time.perf_counter() - ts
@@ -485,7 +546,8 @@ class XPUTrellisEncoder:
     def encode_tensor(self, tiles, pre_permute: bool = False, requested_b: Optional[int] = None,
                       traceback_mode: str = "gpu_resident", finalize: bool = True,
                       allocator_hook: Optional[Callable[[int], None]] = None,
-                      synchronize: bool = True, nan_count=None) -> dict:
+                      synchronize: bool = True, nan_count=None,
+                      traceback_policy: Optional[str] = None) -> dict:
         """Encode an (n, L) float32 device tensor, keeping every output on the
         device. Returns a dict of device tensors: ``x`` (kernel-order fp16
         inputs as f32), ``reconstructed_perm`` (f32, kernel order),
@@ -500,7 +562,10 @@ class XPUTrellisEncoder:
         (its outputs are meaningless, every index stays a valid state).
         ``synchronize=False`` (``gpu_resident`` only) launches everything on
         the current stream and returns without waiting: host ``timings`` stay
-        zero and the scratch buffers are reused in stream order."""
+        zero and the scratch buffers are reused in stream order.
+        ``traceback_policy`` ("auto", "rows", "stream"; None = the process
+        default) picks the traceback kernel of this call (``gpu_resident``);
+        results are identical."""
         import torch
 
         if not isinstance(tiles, torch.Tensor) or tiles.device.type != "cuda":
@@ -527,7 +592,7 @@ class XPUTrellisEncoder:
         out_w = torch.empty((n, self.L), dtype=torch.float32, device=raw.device)
         out_i = torch.empty((n, self.L), dtype=torch.int16, device=raw.device)
         num_chunks = self._run_chunks(ext, x, out_w, out_i, temp_costs, temp_edges, admitted_b,
-                                      traceback_mode, timings, synchronize)
+                                      traceback_mode, timings, synchronize, traceback_policy)
         res = {"x": x, "reconstructed_perm": out_w, "indices": out_i, "admitted_b": admitted_b,
                "num_chunks": num_chunks, "timings": timings}
         if finalize:

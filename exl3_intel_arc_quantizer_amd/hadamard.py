@@ -15,38 +15,42 @@ rounding of the summation order.
 
 from __future__ import annotations
 
+import functools
 import math
 from typing import Optional
 
 import torch
 
 HAD_DIM = 128
-_HAD_CACHE: dict = {}
 
 
 def sylvester_hadamard(n: int) -> torch.Tensor:
-    """Unnormalised Sylvester matrix of order n (+-1, float64), built by the
-    recursion [[h, h], [h, -h]] (hadamard.py:34-54). n must be a power of two."""
+    """Unnormalised Sylvester matrix of order n (+-1, float64; hadamard.py:
+    34-54), from its closed form: entry (i, j) is (-1)^popcount(i & j), the
+    parity of the bits row and column share. n must be a power of two."""
     if n < 1 or (n & (n - 1)) != 0:
         raise ValueError(f"Sylvester construction requires a power-of-two size, got {n}")
-    h = torch.ones((1, 1), dtype=torch.float64)
-    while h.shape[0] < n:
-        h = torch.cat([torch.cat([h, h], dim=1), torch.cat([h, -h], dim=1)], dim=0)
-    return h
+    idx = torch.arange(n, dtype=torch.int64)
+    shared = idx[:, None] & idx[None, :]
+    parity = torch.zeros_like(shared)
+    for bit in range(n.bit_length() - 1):
+        parity ^= (shared >> bit) & 1
+    return (1 - 2 * parity).to(torch.float64)
+
+
+@functools.lru_cache(maxsize=None)
+def _scaled_hadamard(n: int, dtype: torch.dtype, scale: float, device: str) -> torch.Tensor:
+    return (sylvester_hadamard(n) * scale).to(dtype=dtype, device=device)
 
 
 def hadamard(n: int = HAD_DIM, dtype: torch.dtype = torch.float32,
              scale: Optional[float] = None,
              device: Optional[torch.device] = None) -> torch.Tensor:
-    """Orthonormal Sylvester matrix, scale 1/sqrt(n) by default (hadamard.py:57-70)."""
-    if scale is None:
-        scale = 1.0 / math.sqrt(n)
-    key = (n, dtype, float(scale), str(device) if device is not None else "cpu")
-    cached = _HAD_CACHE.get(key)
-    if cached is None:
-        cached = (sylvester_hadamard(n) * scale).to(dtype=dtype, device=device)
-        _HAD_CACHE[key] = cached
-    return cached
+    """Sylvester matrix times ``scale`` (default 1/sqrt(n): orthonormal), in
+    ``dtype`` on ``device`` (hadamard.py:57-70). One tensor per argument set
+    is built and then shared, so callers must not modify it."""
+    factor = 1.0 / math.sqrt(n) if scale is None else float(scale)
+    return _scaled_hadamard(n, dtype, factor, "cpu" if device is None else str(device))
 
 
 def _had128(x: torch.Tensor, side: int, had_dim: int, out: Optional[torch.Tensor]) -> torch.Tensor:

@@ -484,9 +484,11 @@ def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
     encoders = [encode_tiles] + [encode_tiles.fork() for _ in groups[1:]]
     # Tracebacks by per-row tree loads: the streamed kernel reads whole rows,
     # bandwidth the other lane's forward passes need (9B-class layer: 1.20 s
-    # against 1.23-1.26 s). The choice is process-wide while the lanes run.
-    from ._native import set_traceback_policy
-    previous_policy = set_traceback_policy("rows")
+    # against 1.23-1.26 s). Each adapter carries its own choice, so nothing
+    # process-wide changes and other threads' encodes are unaffected.
+    previous_policy = getattr(encode_tiles, "traceback_policy", None)
+    for enc in encoders:
+        enc.traceback_policy = "rows"
     # The first lane stays on the caller's stream: two pool streams can share
     # one hardware queue, which would serialise the lanes again.
     ref = torch.cuda.Event(enable_timing=True)
@@ -522,7 +524,7 @@ def _run_lockstep(walks: List[_Traversal], encode_tiles: TileEncoder,
     finally:
         for lane in lanes[1:]:
             origin.wait_stream(lane.stream)
-        set_traceback_policy(previous_policy)
+        encode_tiles.traceback_policy = previous_policy
         for enc in encoders[1:]:
             enc.encoder.arena.release()
 

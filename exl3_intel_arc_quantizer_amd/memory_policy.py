@@ -53,14 +53,22 @@ ENV_REFLECT_OUTSTANDING = "EXL3_MEMORY_REFLECT_OUTSTANDING"
 _HOST_KEYS = ("MemTotal", "MemFree", "MemAvailable", "Cached", "SwapTotal", "SwapFree",
               "SwapCached")
 _FALSE_WORDS = frozenset(("0", "false", "no", "off"))
+_TRUE_WORDS = frozenset(("1", "true", "yes", "on"))
 
 
 def reflect_outstanding_counters() -> bool:
     """Whether the free-HBM counter already includes this process's live
-    allocations. True unless ``EXL3_MEMORY_REFLECT_OUTSTANDING`` is set to
-    0 / false / no / off."""
+    allocations: True when ``EXL3_MEMORY_REFLECT_OUTSTANDING`` is unset,
+    empty or one of 1 / true / yes / on, False for 0 / false / no / off.
+    Any other value raises ``ValueError``: a misspelt switch must not
+    silently admit more scratch than the operator asked for."""
     value = os.environ.get(ENV_REFLECT_OUTSTANDING, "").strip().lower()
-    return value not in _FALSE_WORDS
+    if value == "" or value in _TRUE_WORDS:
+        return True
+    if value in _FALSE_WORDS:
+        return False
+    raise ValueError(f"{ENV_REFLECT_OUTSTANDING}={value!r} is not one of "
+                     f"{sorted(_TRUE_WORDS | _FALSE_WORDS)}")
 
 
 def default_reserve_bytes() -> int:

@@ -67,7 +67,8 @@ def make_xpu_tile_encoder(K: int = 2, device_index: int = 0, arena=None, sg_size
         res = encoder.encode_tensor(dev_tiles.contiguous(), pre_permute=False,
                                     traceback_mode=traceback_mode, finalize=False,
                                     synchronize=not run_async,
-                                    nan_count=state["nan_count"] if run_async else None)
+                                    nan_count=state["nan_count"] if run_async else None,
+                                    traceback_policy=encode.traceback_policy)
         recon, idx = res["reconstructed_perm"], res["indices"]
         if not on_device:
             recon, idx = recon.to(tiles.device), idx.to(tiles.device)
@@ -87,6 +88,10 @@ def make_xpu_tile_encoder(K: int = 2, device_index: int = 0, arena=None, sg_size
 
     encode.K = K
     encode.cb = cb
+    # Traceback kernel of this adapter's calls ("auto", "rows", "stream";
+    # None = the library's process default). Per adapter, so two lanes on
+    # two streams can choose differently.
+    encode.traceback_policy = None
     encode.encoder = encoder
     encode.check_finite = check_finite
     encode.fork = fork

@@ -51,11 +51,12 @@ const char* exl3_last_error(void);
 /* Library version string. */
 const char* exl3_version(void);
 
-/* Traceback kernel choice for every later call in this process (no
- * counterpart in the reference, whose traceback has one form): 0 = by
- * batch size (default), 1 = per-row tree loads, 2 = whole rows streamed
- * through LDS. Both kernels give identical results. Returns the previous
- * policy, or -1 for a value outside 0..2. */
+/* Default traceback kernel for later calls in this process that do not
+ * choose one per call (no counterpart in the reference, whose traceback has
+ * one form): 0 = by batch size (default), 1 = per-row tree loads, 2 = whole
+ * rows streamed through LDS. Both kernels give identical results. The
+ * default is an atomic; exl3_quantize_tiles_tb chooses per call instead.
+ * Returns the previous policy, or -1 for a value outside 0..2. */
 int exl3_set_traceback_policy(int policy);
 
 /* Replaces decode_codebook (quantize_xpu.cpp:105-110,
@@ -85,6 +86,17 @@ int64_t exl3_cost_row_slot(int K, int64_t edge);
 int exl3_quantize_tiles(const float* in, float* out_w, int16_t* out_idx, uint16_t* temp_costs,
                         uint8_t* temp_edges, int64_t batch_cap, int64_t n, int K, int cb, int L,
                         int generic, int64_t wave_cap, void* stream);
+
+/* exl3_quantize_tiles with the traceback kernel chosen for this call only
+ * (no counterpart in the reference, whose traceback has one form):
+ * traceback = 0 by batch size, 1 per-row tree loads, 2 whole rows streamed
+ * through LDS, -1 the process default of exl3_set_traceback_policy. Results
+ * are identical for every choice; the process default is not changed, so
+ * callers on several threads or streams may choose differently. */
+int exl3_quantize_tiles_tb(const float* in, float* out_w, int16_t* out_idx,
+                           uint16_t* temp_costs, uint8_t* temp_edges, int64_t batch_cap,
+                           int64_t n, int K, int cb, int L, int generic, int64_t wave_cap,
+                           int traceback, void* stream);
 
 /* Bytes of the library's static scratch for exl3_quantize_tiles_noalloc. */
 #define EXL3_NOALLOC_SCRATCH_BYTES ((int64_t)512 << 20)

@@ -82,17 +82,32 @@ def test_batch_halving_and_clean_rejection(torch_mod):
         XPUTrellisEncoder(K=2, cb=2, arena=impossible).encode_batch(tiles, requested_b=4)
     assert impossible.resident_bytes == 0
 
-    # A single-allocation ceiling caps B: here at 4 tiles' worth of edges.
-    per_b = ScratchEstimator.estimate_scratch(k=3, b=1, t=256).edges_bytes
-    ceiling = ScratchArena(policy=MemoryPolicy(reserve_bytes=4 * BYTES_PER_GIB,
-                                               max_single_alloc_bytes=4 * per_b))
-    try:
-        assert ceiling.adaptive_batch_capacity(k=3, requested_b=16) == 4
-        _, _, adm = ceiling.acquire(k=3, requested_b=16)
-        assert adm == 4
-    finally:
-        ceiling.release()
+    # A single-allocation ceiling caps B. A slot is one allocation (terminal
+    # costs and cost rows together), so the ceiling counts a tile's whole
+    # scratch: here 4 tiles' worth, and 3.5 tiles' worth admits 3 (query)
+    # and 2 (halving from 16).
+    per_b = ScratchEstimator.estimate_scratch(k=3, b=1, t=256).total_bytes
+    for limit, query, halved in ((4 * per_b, 4, 4), (7 * per_b // 2, 3, 2)):
+        ceiling = ScratchArena(policy=MemoryPolicy(reserve_bytes=4 * BYTES_PER_GIB,
+                                                   max_single_alloc_bytes=limit))
+        try:
+            assert ceiling.adaptive_batch_capacity(k=3, requested_b=16) == query
+            costs, edges, adm = ceiling.acquire(k=3, requested_b=16)
+            assert adm == halved
+            assert ceiling.resident_bytes == halved * per_b <= limit
+            # Both views live in the one slot, costs first, rows after.
+            assert costs.shape == (halved, 2, 65536 >> 3) and edges.shape[0] == halved
+            assert edges.data_ptr() == costs.data_ptr() + costs.numel() * 2
+        finally:
+            ceiling.release()
     assert 4 * per_b < 64 * BYTES_PER_MIB
+    tiny = ScratchArena(policy=MemoryPolicy(reserve_bytes=4 * BYTES_PER_GIB,
+                                            max_single_alloc_bytes=per_b - 1))
+    with pytest.raises(MemoryPressureError, match="ceiling"):
+        tiny.adaptive_batch_capacity(k=3, requested_b=16)
+    with pytest.raises(MemoryPressureError, match="ceiling"):
+        tiny.acquire(k=3, requested_b=16)
+    assert tiny.resident_bytes == 0 and tiny.retries == 4     # 16, 8, 4, 2 -> 1
 
 
 def test_retry_path_holds_one_attempt_at_a_time(torch_mod):

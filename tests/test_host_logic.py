@@ -93,8 +93,15 @@ def test_policy_env_overrides(monkeypatch):
     monkeypatch.delenv("EXL3_MEMORY_RESERVE_BYTES")
     assert default_reserve_bytes() == 8 * BYTES_PER_GIB
     assert reflect_outstanding_counters() is True
-    monkeypatch.setenv("EXL3_MEMORY_REFLECT_OUTSTANDING", "0")
-    assert reflect_outstanding_counters() is False
+    for word, want in (("0", False), ("off", False), ("No", False), ("1", True),
+                       (" TRUE ", True), ("on", True), ("", True)):
+        monkeypatch.setenv("EXL3_MEMORY_REFLECT_OUTSTANDING", word)
+        assert reflect_outstanding_counters() is want, word
+    # A misspelt switch is an error, not a silent "on".
+    for word in ("disable", "2", "tru"):
+        monkeypatch.setenv("EXL3_MEMORY_REFLECT_OUTSTANDING", word)
+        with pytest.raises(ValueError, match="EXL3_MEMORY_REFLECT_OUTSTANDING"):
+            reflect_outstanding_counters()
 
 
 def test_package_perm_matches_oracle():
