@@ -279,7 +279,17 @@ struct RowGather {
       constexpr int HALF = PIECES / 2;
       static_assert(HALF <= NT && HALF % 64 == 0, "one pair of pieces per thread");
       const int tid = threadIdx.x;
-      const int c = (tid & ~63) | ((tid & 31) << 1) | ((tid >> 5) & 1);
+      int c;
+      if constexpr (K == 2) {
+        // Piece index bits 0..9 are positions 3..12 = edge bits x11, x4 ..
+        // x9, x1, x2, x3. A half-wave spans x1 .. x5 (the dword's bank), the
+        // two halves differ in x11, the 16 waves in x6 .. x9: each half-wave
+        // reads 32 banks, and a wave stores 8 whole 128-byte lines.
+        const int lane = tid & 63, w = tid >> 6;
+        c = ((lane >> 5) & 1) | ((lane & 24) >> 2) | ((lane & 7) << 7) | ((w & 15) << 3);
+      } else {
+        c = (tid & ~63) | ((tid & 31) << 1) | ((tid >> 5) & 1);
+      }
       if (HALF == NT || tid < HALF) {
         const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
         uint32_t r[8];
@@ -327,10 +337,11 @@ __device__ __forceinline__ bool stores_row(const FwdArgs& a, int K, int i) {
 template <int K, int B>
 __device__ __forceinline__ bool stores_row_at(const FwdArgs& a, int i) {
   constexpr int STRIDE = exl3::row_stride(K);
-  if constexpr (STRIDE > 1 && B == 0) {
+  if constexpr (STRIDE > 1 && STRIDE % 2 == 0 && B == 0) {
     return false;
   } else {
-    return i - 1 >= a.store_from && (STRIDE <= 2 || (i - 1) % STRIDE == 0);
+    return i - 1 >= a.store_from &&
+           (STRIDE == 1 || (STRIDE == 2 && B == 1) || (i - 1) % STRIDE == 0);
   }
 }
 
@@ -1100,7 +1111,9 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, ui
   constexpr int RLOG = NLOG > 6 ? NLOG - 6 : 0;
   constexpr int R = 1 << RLOG;
   constexpr uint32_t NMASK = (1u << NLOG) - 1u;
-  constexpr int CH = R < NB ? R : NB;
+  // A lane's R leaves are one aligned run in K = 2's tree-major rows, and
+  // its 2^K siblings elsewhere.
+  constexpr int CH = (K == 2 || R < NB) ? R : NB;
   const uint32_t h0 = edge >> K;
 
   uint32_t nid[R];
@@ -1126,9 +1139,9 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, ui
 #pragma unroll
     for (int u = 0; u < CH; ++u) v[c * CH + u] = q[u];
   }
-  // A lane's leaves are at most 8 bytes (R <= 4) with every K's stride:
-  // one load per tree and lane.
-  static_assert(R <= 4, "one load of siblings per lane");
+  // A lane's leaves are at most 8 bytes (R <= 4) at every K but 2, whose
+  // 16 (32 bytes, two loads) are one aligned run.
+  static_assert(R <= 4 || (K == 2 && R <= 16), "a lane's leaves are one run");
 
   uint32_t lvl[D > 0 ? D : 1][R];
 #pragma unroll

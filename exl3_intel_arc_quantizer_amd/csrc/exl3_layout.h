@@ -21,8 +21,8 @@
 //   of step i-1 (the costs the forward step i read). A row is group-major:
 //   predecessor edge x = (k << (16-2K)) | h sits at position (h << K) | k,
 //   so the 2^K costs one traceback step reads are one contiguous chunk
-//   (K = 2..5 also keep part of the digit before beside it, see
-//   cost_row_pos).
+//   (K = 3, 4 also keep part of the digit before beside it, and K = 2 keeps
+//   whole traceback trees together, see cost_row_pos).
 //   Only every row_stride(K)-th step is stored (8 KiB or less of HBM writes
 //   per step at K <= 5, every step at K >= 6, where a row is 2 KiB or less);
 //   for a step d rows past the last stored one, the
@@ -56,12 +56,16 @@ struct RowLayout {
 };
 
 // Steps between stored cost rows: about 8 KiB of HBM writes per step at
-// K <= 4, every step at K >= 5 (where a row is 4 KiB or less). At K = 5
-// every-step rows double the forward pass's writes but cut the traceback's
-// trees from 1024 costs to 32: a whole encode is faster at every batch size
-// (8192 tiles -2 %, 256 tiles -6 %).
+// K = 1, 3, 4, 6.4 KiB at K = 2, every step at K >= 5 (where a row is 4 KiB
+// or less). At K = 5 every-step rows double the forward pass's writes but
+// cut the traceback's trees from 1024 costs to 32: a whole encode is faster
+// at every batch size (8192 tiles -2 %, 256 tiles -6 %). At K = 2 stride 5
+// (trees of 1024 costs, kept whole by the tree-major row layout) writes 20 %
+// less than stride 4: the forward pass runs 2-4 % faster, which outweighs
+// the larger trees (whole encodes -1 to -2.4 % at 1024-8192 tiles, equal at
+// 256).
 EXL3_HD constexpr inline int row_stride(int K) {
-  return K == 1 ? 8 : (K == 2 ? 4 : (K <= 4 ? 2 : 1));
+  return K == 1 ? 8 : (K == 2 ? 5 : (K <= 4 ? 2 : 1));
 }
 
 // The fast forward kernels cover K = 1..8: an edge-order kernel for K = 1..3
@@ -84,20 +88,34 @@ EXL3_HD inline RowLayout make_layout(int K) {
 EXL3_HD inline bool cost_row_stored(const RowLayout& l, int step) { return step % l.stride == 0; }
 EXL3_HD inline int cost_row_slot(const RowLayout& l, int step) { return step / l.stride; }
 // Group-major: x = (k << (16-2K)) | h at (h << K) | k, so the 2^K costs a
-// traceback step compares are one chunk. At K = 2..4, where a stored row
-// serves several steps and one traceback tree spans 2^(K * stride)
-// entries, the row also keeps part of the digit before k beside it: the
-// last digit (x >> (16-2K)) at positions [0, K), then the lowest
-// cost_row_tree_bits(K) bits of the digit before it, then the other bits of
-// x from bit 1 up, and x bit 0 on top. A tree then covers 16 (K = 2) or
-// 4 (K = 3, 4) cache lines instead of 64, 8 or 16, and positions t and
-// t + E/2 hold the neighbouring edges x and x + 1 (one dword in the
-// edge-order LDS vector of K = 2, 3). More bits of that digit would put
-// that kernel's LDS gather into bank conflicts.
+// traceback step compares are one chunk. At K = 3, 4, where a stored row
+// serves two steps and one traceback tree spans 2^(2K) entries, the row
+// also keeps part of the digit before k beside it: the last digit
+// (x >> (16-2K)) at positions [0, K), then the lowest cost_row_tree_bits(K)
+// bits of the digit before it, then the other bits of x from bit 1 up, and
+// x bit 0 on top. A tree then covers 4 cache lines instead of 8 or 16, and
+// at K = 3 positions t and t + E/2 hold the neighbouring edges x and x + 1
+// (one dword in the edge-order LDS vector). More bits of that digit would
+// put that kernel's LDS gather into bank conflicts.
+//
+// K = 2 (stride 5) is tree-major: position bit j holds edge bit
+// kRowBitsK2[j]. The 10 edge bits a 5-step traceback tree spans (x4..x13)
+// are positions 0..9, last digit first, so a tree is one aligned run of
+// 1024 positions (2 KiB, 16 cache lines; the group-major order spread it
+// over 64); the fixed bits x1..x3 follow and x0 is on top, so the LDS
+// neighbours x, x + 1 again sit at positions t, t + E/2. The forward pass's
+// gather keeps its LDS reads conflict-free by giving each half-wave pieces
+// that differ in x1..x5 (RowGather).
 EXL3_HD constexpr inline int cost_row_tree_bits(int K) {
-  return K == 2 ? 2 : (K == 3 ? 1 : (K == 4 ? 2 : 0));
+  return K == 2 ? 10 : (K == 3 ? 1 : (K == 4 ? 2 : 0));
 }
+constexpr int kRowBitsK2[14] = {12, 13, 10, 11, 4, 5, 6, 7, 8, 9, 1, 2, 3, 0};
 EXL3_HD inline uint32_t cost_row_pos(int K, uint32_t x) {
+  if (K == 2) {
+    uint32_t t = 0;
+    for (int j = 0; j < 14; ++j) t |= ((x >> kRowBitsK2[j]) & 1u) << j;
+    return t;
+  }
   const int ks = 16 - 2 * K;
   const int a = cost_row_tree_bits(K);
   if (a == 0) return ((x & ((1u << ks) - 1u)) << K) | (x >> ks);
@@ -109,6 +127,11 @@ EXL3_HD inline uint32_t cost_row_pos(int K, uint32_t x) {
 }
 // The edge at position t of a stored row (the inverse of cost_row_pos).
 EXL3_HD inline uint32_t cost_row_edge(int K, uint32_t t) {
+  if (K == 2) {
+    uint32_t x = 0;
+    for (int j = 0; j < 14; ++j) x |= ((t >> j) & 1u) << kRowBitsK2[j];
+    return x;
+  }
   const int ks = 16 - 2 * K;
   const int a = cost_row_tree_bits(K);
   if (a == 0) return ((t & ((1u << K) - 1u)) << ks) | (t >> K);

@@ -23,7 +23,7 @@
  *                                          E = 65536 >> K (same as reference)
  *   temp_edges : bytes [B][ROWS][ROWB]    per tile, the fp16 path costs
  *                                          after every S-th step
- *                                          (S = 8, 4, 2, 2, 1, 1, 1, 1 for
+ *                                          (S = 8, 5, 2, 2, 1, 1, 1, 1 for
  *                                          K = 1..8; ROWB = 2E, group-major),
  *                                          then the header (the L inputs and
  *                                          three int32 fields).
@@ -108,7 +108,7 @@ int exl3_quantize_tiles_tb(const float* in, float* out_w, int16_t* out_idx,
  * MiB) that each GPU holds from library load until the process ends. No
  * hipMalloc, hipFree or allocating library call is made. Limit: all n tiles
  * must fit at once, n <= floor((EXL3_NOALLOC_SCRATCH_BYTES - 255) /
- * (4 (65536 >> K) + exl3_scratch_edges_bytes(K, L, 1))), e.g. 244 tiles at
+ * (4 (65536 >> K) + exl3_scratch_edges_bytes(K, L, 1))), e.g. 303 tiles at
  * K = 2 and 500 at K = 4 (L = 256); larger n is rejected with an error and
  * nothing is launched. Every call on one GPU shares that GPU's array: calls
  * that overlap on one GPU (on different streams, or from several threads
