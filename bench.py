@@ -416,12 +416,17 @@ def run_layer_config(torch, K=4, gss=False):
             "cpu_path_parity": None if gss else layer_cpu_parity(res, H)}
 
 
-def run_decoder_config(torch, K=4, cpu_tiles_per_s=None, lockstep=True, gss=False):
+def run_decoder_config(torch, K=4, cpu_tiles_per_s=None, lockstep=True, gss=False,
+                       profile_window=False):
     """configs[4]: a 9B-class decoder layer (hidden 4096; q, o 4096x4096;
     k, v 1024x4096; gate, up 12288x4096; down 4096x12288), random-init weights
     (torch seed 5), Hessians per shared-input group from synthetic bf16
     activations [16384, width] (seeds 6..9, 5 % of channels x10), K = 4:
-    753,664 tiles in 2,304 encoder calls."""
+    753,664 tiles in 2,304 encoder calls. ``profile_window``: for a
+    rocprofv3 kernel trace, a 1-second host pause (a gap in the trace)
+    separates the warm-up conversion from the timed one, and the
+    events-timed third conversion is skipped, so the window after the gap
+    is exactly one conversion."""
     from exl3_intel_arc_quantizer_amd.layer_quant import (hessian_from_activations,
                                                           hessian_groups,
                                                           quantize_decoder_layer)
@@ -457,9 +462,18 @@ def run_decoder_config(torch, K=4, cpu_tiles_per_s=None, lockstep=True, gss=Fals
     first = quantize_decoder_layer(layer, hess, K=K, lockstep=lockstep, skip_g_scale=not gss)
     first_wall = first.total_elapsed_seconds
     del first
+    if profile_window:
+        torch.cuda.synchronize()
+        time.sleep(1.0)
     rep = quantize_decoder_layer(layer, hess, K=K, lockstep=lockstep, skip_g_scale=not gss)
     wall = rep.total_elapsed_seconds
     calls = sum(r.metrics.encoder_calls for r in rep.module_results.values())
+    if profile_window:
+        return {"metric": "9B-class decoder layer conversion (profile window), K=4",
+                "value": round(wall, 3), "unit": "s", "first_layer_seconds": round(first_wall, 3),
+                "phases": {k: round(v, 3) for k, v in rep.extra.items()
+                           if k.endswith("_seconds")},
+                "module_encoder_calls": calls, "tiles": rep.tiles}
     # The encoder's share from a third conversion that times every call with
     # HIP events (about 5 us of stream time per call).
     timed = quantize_decoder_layer(layer, hess, K=K, lockstep=lockstep, skip_g_scale=not gss,
@@ -662,6 +676,10 @@ def main() -> int:
                     help="only the API-level rates, printed as their own JSON line")
     ap.add_argument("--gss", action="store_true",
                     help="with --layer / --decoder: run the global-scale search (skip_g_scale=False)")
+    ap.add_argument("--profile-decoder", action="store_true",
+                    help="with --decoder: pause 1 s between the warm-up and the measured "
+                         "conversion and skip the events-timed one (one conversion per trace "
+                         "window)")
     ap.add_argument("--sequential", action="store_true",
                     help="with --decoder: one projection at a time (the reference's order)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -709,7 +727,9 @@ def main() -> int:
         if args.decoder:
             print(json.dumps(run_decoder_config(torch, cpu_tiles_per_s=cpu["value"] if cpu
                                                 else None, lockstep=not args.sequential,
-                                                gss=args.gss)), flush=True)
+                                                gss=args.gss,
+                                                profile_window=args.profile_decoder)),
+                  flush=True)
         return 0
 
     if args.calibrate_copy:
