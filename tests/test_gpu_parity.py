@@ -367,6 +367,57 @@ def test_traceback_kernels_agree(K):
         _native.set_traceback_policy(prev)
 
 
+def test_per_call_traceback_choice_threads():
+    """exl3_quantize_tiles_tb: every per-call traceback choice gives the
+    oracle's states; two threads encoding at once on two streams with
+    different choices both do, and neither changes the process default."""
+    import threading
+
+    import torch
+
+    from exl3_intel_arc_quantizer_amd import _native
+    from exl3_intel_arc_quantizer_amd._native import QuantizeExtension, edges_shape
+    K = 4
+    rng = np.random.default_rng(777)
+    tiles = rng.normal(0.0, 1.0, size=(64, 256)).astype(np.float32)
+    ref = c_oracle.encode_tiles(tiles, K=K, cb=2, pre_permute=False)
+    x = torch.from_numpy(tiles.astype(np.float16).astype(np.float32)).cuda()
+    ext = QuantizeExtension()
+
+    def encode(policy, out, stream):
+        with torch.cuda.stream(stream):
+            costs = torch.empty((64, 2, 65536 >> K), dtype=torch.float16, device="cuda")
+            edges = torch.empty(edges_shape(64, K), dtype=torch.uint8, device="cuda")
+            w = torch.empty((64, 256), dtype=torch.float32, device="cuda")
+            i = torch.empty((64, 256), dtype=torch.int16, device="cuda")
+            for _ in range(4):
+                ext.quantize_tiles(x, w, i, costs, edges, K, False, True,
+                                   traceback_policy=policy)
+            stream.synchronize()
+            out[policy] = i.cpu().numpy().view(np.uint16)
+
+    prev = _native.set_traceback_policy("auto")
+    try:
+        out = {}
+        for policy in (None, "auto", "rows", "stream"):
+            print(f"per-call traceback={policy}", flush=True)
+            encode(policy, out, torch.cuda.current_stream())
+            np.testing.assert_array_equal(out[policy], ref.output_indices, err_msg=str(policy))
+        print("two threads: rows and stream", flush=True)
+        out = {}
+        threads = [threading.Thread(target=encode, args=(p, out, torch.cuda.Stream()))
+                   for p in ("rows", "stream")]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        for policy in ("rows", "stream"):
+            np.testing.assert_array_equal(out[policy], ref.output_indices, err_msg=policy)
+        assert _native.set_traceback_policy("auto") == "auto"
+    finally:
+        _native.set_traceback_policy(prev)
+
+
 def test_traceback_modes_and_variants_agree():
     """tests/test_xpu_quantizer.py:299-330."""
     rng = np.random.default_rng(909)

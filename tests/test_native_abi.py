@@ -168,6 +168,29 @@ def test_traceback_policy_switch():
         _native.set_traceback_policy("fast")
 
 
+def test_per_call_traceback_choice_is_checked_on_the_host():
+    """exl3_quantize_tiles_tb rejects a traceback choice outside -1..2 before
+    any launch (dummy non-NULL pointers never reach a kernel), leaves the
+    process default alone, and the Python facade rejects an unknown name
+    before it looks at the tensors."""
+    import torch
+    lib = _native.load_library()
+    p = 16
+    assert _native.set_traceback_policy("rows") == "auto"
+    try:
+        for bad in (3, -2):
+            assert lib.exl3_quantize_tiles_tb(p, p, p, p, p, 4, 4, 4, 2, 256, 0, 0, bad,
+                                              None) != 0
+            assert b"traceback must be -1, 0, 1 or 2" in lib.exl3_last_error()
+        assert _native.set_traceback_policy("auto") == "rows"
+    finally:
+        _native.set_traceback_policy("auto")
+    t = torch.zeros((1, 256), dtype=torch.float32)
+    with pytest.raises(ValueError, match="policy must be one of"):
+        _native.QuantizeExtension().quantize_tiles(t, t, t, t, t, 2, False, True,
+                                                   traceback_policy="fast")
+
+
 def test_layer_entry_points_reject_bad_arguments():
     """include/exl3_layer.h: every argument check runs on the host, before
     any launch (dummy non-NULL pointers never reach a kernel here)."""
