@@ -268,27 +268,29 @@ struct RowGather {
     vec* dst = reinterpret_cast<vec*>(a.scratch + (int64_t)blockIdx.x * a.tile_stride +
                                       (int64_t)exl3::cost_row_slot(lay, step) * lay.row_bytes);
     if constexpr (K > 1) {
-      static_assert(exl3::cost_row_tree_bits(K) > 0, "K = 2, 3 rows keep tree bits");
+      static_assert(exl3::cost_row_tree_bits(K) > 0, "K = 2, 3 rows are tree-major");
       // Positions t and t + E/2 hold the LDS neighbours x and x + 1 (x
       // even): the first E/16 threads take pieces c and c + E/16 each, from
       // eight dword reads, their halves sorted into the two pieces by
-      // v_perm. Lane l of a wave takes piece 2 (l mod 32) + l / 32 of the
-      // wave's 64: piece bit 0 selects a far LDS bank row, so each half-wave
-      // reads 32 different banks, and the wave's store is still one
-      // contiguous kilobyte.
+      // v_perm. A dword's LDS bank is edge bits x1 .. x6, so each half-wave
+      // takes the 32 pieces that differ in x1 .. x5 (32 different banks per
+      // read), and a wave's 64 pieces are 8 runs of 8: 8 whole 128-byte
+      // lines per store.
       constexpr int HALF = PIECES / 2;
       static_assert(HALF <= NT && HALF % 64 == 0, "one pair of pieces per thread");
       const int tid = threadIdx.x;
+      const int lane = tid & 63, w = tid >> 6;
       int c;
       if constexpr (K == 2) {
-        // Piece index bits 0..9 are positions 3..12 = edge bits x11, x4 ..
-        // x9, x1, x2, x3. A half-wave spans x1 .. x5 (the dword's bank), the
-        // two halves differ in x11, the 16 waves in x6 .. x9: each half-wave
-        // reads 32 banks, and a wave stores 8 whole 128-byte lines.
-        const int lane = tid & 63, w = tid >> 6;
+        // Piece bits 0..9 are positions 3..12 = edge bits x11, x4 .. x9, x1,
+        // x2, x3: a half-wave spans x1 .. x5, its halves differ in x11, the
+        // 16 waves in x6 .. x9.
         c = ((lane >> 5) & 1) | ((lane & 24) >> 2) | ((lane & 7) << 7) | ((w & 15) << 3);
       } else {
-        c = (tid & ~63) | ((tid & 31) << 1) | ((tid >> 5) & 1);
+        // Piece bits 0..8 are positions 3..11 = edge bits x4 .. x9, x1, x2,
+        // x3: a half-wave spans x1 .. x5, its halves differ in x6, the 8
+        // gathering waves in x7 .. x9.
+        c = (lane & 3) | ((lane & 28) << 4) | (((lane >> 5) & 1) << 2) | ((w & 7) << 3);
       }
       if (HALF == NT || tid < HALF) {
         const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
@@ -1113,7 +1115,7 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, ui
   constexpr uint32_t NMASK = (1u << NLOG) - 1u;
   // A lane's R leaves are one aligned run in K = 2's tree-major rows, and
   // its 2^K siblings elsewhere.
-  constexpr int CH = (K == 2 || R < NB) ? R : NB;
+  constexpr int CH = (K == 2 || K == 3 || R < NB) ? R : NB;
   const uint32_t h0 = edge >> K;
 
   uint32_t nid[R];
@@ -1141,7 +1143,7 @@ __device__ __forceinline__ uint32_t tb_tree(const uint16_t* __restrict__ row, ui
   }
   // A lane's leaves are at most 8 bytes (R <= 4) at every K but 2, whose
   // 16 (32 bytes, two loads) are one aligned run.
-  static_assert(R <= 4 || (K == 2 && R <= 16), "a lane's leaves are one run");
+  static_assert(R <= 4 || ((K == 2 || K == 3) && R <= 16), "a lane's leaves are one run");
 
   uint32_t lvl[D > 0 ? D : 1][R];
 #pragma unroll

@@ -21,7 +21,7 @@
 //   of step i-1 (the costs the forward step i read). A row is group-major:
 //   predecessor edge x = (k << (16-2K)) | h sits at position (h << K) | k,
 //   so the 2^K costs one traceback step reads are one contiguous chunk
-//   (K = 3, 4 also keep part of the digit before beside it, and K = 2 keeps
+//   (K = 4 also keeps part of the digit before beside it, and K = 2, 3 keep
 //   whole traceback trees together, see cost_row_pos).
 //   Only every row_stride(K)-th step is stored (8 KiB or less of HBM writes
 //   per step at K <= 5, every step at K >= 6, where a row is 2 KiB or less);
@@ -55,17 +55,17 @@ struct RowLayout {
   int32_t reserved;
 };
 
-// Steps between stored cost rows: about 8 KiB of HBM writes per step at
-// K = 1, 3, 4, 6.4 KiB at K = 2, every step at K >= 5 (where a row is 4 KiB
-// or less). At K = 5 every-step rows double the forward pass's writes but
-// cut the traceback's trees from 1024 costs to 32: a whole encode is faster
-// at every batch size (8192 tiles -2 %, 256 tiles -6 %). At K = 2 stride 5
-// (trees of 1024 costs, kept whole by the tree-major row layout) writes 20 %
-// less than stride 4: the forward pass runs 2-4 % faster, which outweighs
-// the larger trees (whole encodes -1 to -2.4 % at 1024-8192 tiles, equal at
-// 256).
+// Steps between stored cost rows: 8 KiB of HBM writes per step at K = 1,
+// 6.4 KiB at K = 2, 5.3 KiB at K = 3, 4 KiB at K = 4, every step at K >= 5
+// (where a row is 4 KiB or less). At K = 5 every-step rows double the
+// forward pass's writes but cut the traceback's trees from 1024 costs to
+// 32: a whole encode is faster at every batch size (8192 tiles -2 %, 256
+// tiles -6 %). At K = 2 stride 5 and at K = 3 stride 3 (trees of 1024 and
+// 512 costs, each kept whole by a tree-major row layout) write 20 % and
+// 33 % less than strides 4 and 2: whole encodes -1 to -2.4 % (K = 2) and
+// -2.5 to -8.3 % (K = 3) at 256-8192 tiles.
 EXL3_HD constexpr inline int row_stride(int K) {
-  return K == 1 ? 8 : (K == 2 ? 5 : (K <= 4 ? 2 : 1));
+  return K == 1 ? 8 : (K == 2 ? 5 : (K == 3 ? 3 : (K == 4 ? 2 : 1)));
 }
 
 // The fast forward kernels cover K = 1..8: an edge-order kernel for K = 1..3
@@ -88,32 +88,37 @@ EXL3_HD inline RowLayout make_layout(int K) {
 EXL3_HD inline bool cost_row_stored(const RowLayout& l, int step) { return step % l.stride == 0; }
 EXL3_HD inline int cost_row_slot(const RowLayout& l, int step) { return step / l.stride; }
 // Group-major: x = (k << (16-2K)) | h at (h << K) | k, so the 2^K costs a
-// traceback step compares are one chunk. At K = 3, 4, where a stored row
+// traceback step compares are one chunk. At K = 4, where a stored row
 // serves two steps and one traceback tree spans 2^(2K) entries, the row
 // also keeps part of the digit before k beside it: the last digit
 // (x >> (16-2K)) at positions [0, K), then the lowest cost_row_tree_bits(K)
 // bits of the digit before it, then the other bits of x from bit 1 up, and
-// x bit 0 on top. A tree then covers 4 cache lines instead of 8 or 16, and
-// at K = 3 positions t and t + E/2 hold the neighbouring edges x and x + 1
-// (one dword in the edge-order LDS vector). More bits of that digit would
-// put that kernel's LDS gather into bank conflicts.
+// x bit 0 on top. A tree then covers 4 cache lines instead of 16.
 //
-// K = 2 (stride 5) is tree-major: position bit j holds edge bit
-// kRowBitsK2[j]. The 10 edge bits a 5-step traceback tree spans (x4..x13)
-// are positions 0..9, last digit first, so a tree is one aligned run of
-// 1024 positions (2 KiB, 16 cache lines; the group-major order spread it
-// over 64); the fixed bits x1..x3 follow and x0 is on top, so the LDS
-// neighbours x, x + 1 again sit at positions t, t + E/2. The forward pass's
-// gather keeps its LDS reads conflict-free by giving each half-wave pieces
-// that differ in x1..x5 (RowGather).
+// K = 2 (stride 5) and K = 3 (stride 3) are tree-major: position bit j holds
+// edge bit kRowBitsK2[j] / kRowBitsK3[j]. The edge bits a traceback tree
+// spans (x4..x13 at K = 2, x4..x12 at K = 3) are the low positions, last
+// digit first, so a tree is one aligned run of 1024 / 512 positions (2 KiB
+// or 1 KiB; the group-major order spread a K = 2 tree over 64 cache lines);
+// the fixed bits x1..x3 follow and x0 is on top, so the edge-order LDS
+// neighbours x, x + 1 sit at positions t, t + E/2 (one dword, two pieces,
+// for the forward pass's gather). That gather keeps its LDS reads
+// conflict-free by giving each half-wave pieces that differ in x1..x5
+// (RowGather).
 EXL3_HD constexpr inline int cost_row_tree_bits(int K) {
-  return K == 2 ? 10 : (K == 3 ? 1 : (K == 4 ? 2 : 0));
+  return K == 2 ? 10 : (K == 3 ? 9 : (K == 4 ? 2 : 0));
 }
 constexpr int kRowBitsK2[14] = {12, 13, 10, 11, 4, 5, 6, 7, 8, 9, 1, 2, 3, 0};
+constexpr int kRowBitsK3[13] = {10, 11, 12, 4, 5, 6, 7, 8, 9, 1, 2, 3, 0};
 EXL3_HD inline uint32_t cost_row_pos(int K, uint32_t x) {
   if (K == 2) {
     uint32_t t = 0;
     for (int j = 0; j < 14; ++j) t |= ((x >> kRowBitsK2[j]) & 1u) << j;
+    return t;
+  }
+  if (K == 3) {
+    uint32_t t = 0;
+    for (int j = 0; j < 13; ++j) t |= ((x >> kRowBitsK3[j]) & 1u) << j;
     return t;
   }
   const int ks = 16 - 2 * K;
@@ -130,6 +135,11 @@ EXL3_HD inline uint32_t cost_row_edge(int K, uint32_t t) {
   if (K == 2) {
     uint32_t x = 0;
     for (int j = 0; j < 14; ++j) x |= ((t >> j) & 1u) << kRowBitsK2[j];
+    return x;
+  }
+  if (K == 3) {
+    uint32_t x = 0;
+    for (int j = 0; j < 13; ++j) x |= ((t >> j) & 1u) << kRowBitsK3[j];
     return x;
   }
   const int ks = 16 - 2 * K;

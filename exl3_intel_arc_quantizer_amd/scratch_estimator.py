@@ -7,7 +7,7 @@ and method names. The formula changes with the layout
     S      = 65536 >> K                      edges per step
     row    = S * 2                           one fp16 cost per edge
     rows   = (T - 2) // stride + 1           every stride-th step
-                                             (stride 8, 5, 2, 2, 1, 1, 1, 1)
+                                             (stride 8, 5, 3, 2, 1, 1, 1, 1)
            + ceil((16 + 2 T) / row)          header: fields and the T inputs
                                              (one row; two at K = 8)
     costs  = B * 2 * S * 2                   terminal fp16 costs of both passes
@@ -15,7 +15,7 @@ and method names. The formula changes with the layout
 
 The reference's int16 layout, ``B * T * S * 2``, is still available by
 passing ``bytes_per_edge`` explicitly (e.g. to compare the two). Per tile at
-T = 256: K=1 2.06 MiB (reference 16 MiB), K=2 1.63 MiB (8 MiB), K=3 2.02 MiB
+T = 256: K=1 2.06 MiB (reference 16 MiB), K=2 1.63 MiB (8 MiB), K=3 1.34 MiB
 (4 MiB), K=4 1.01 MiB (2 MiB), K=5 1 MiB (1 MiB), K=6 512 KiB (512 KiB),
 K=7 256 KiB (256 KiB), K=8 128.5 KiB (128 KiB).
 """
@@ -44,7 +44,7 @@ def uses_cost_rows(k: int) -> bool:
 
 def row_stride(k: int) -> int:
     """Steps between stored cost rows (exl3_layout.h row_stride)."""
-    return {1: 8, 2: 5, 3: 2, 4: 2}.get(k, 1)
+    return {1: 8, 2: 5, 3: 3, 4: 2}.get(k, 1)
 
 
 COST_BITS = 16  # one fp16 cost per edge and stored row

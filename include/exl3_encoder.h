@@ -23,7 +23,7 @@
  *                                          E = 65536 >> K (same as reference)
  *   temp_edges : bytes [B][ROWS][ROWB]    per tile, the fp16 path costs
  *                                          after every S-th step
- *                                          (S = 8, 5, 2, 2, 1, 1, 1, 1 for
+ *                                          (S = 8, 5, 3, 2, 1, 1, 1, 1 for
  *                                          K = 1..8; ROWB = 2E, group-major),
  *                                          then the header (the L inputs and
  *                                          three int32 fields).

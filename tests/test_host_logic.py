@@ -32,7 +32,7 @@ def test_reference_formula_fixtures_still_reproducible():
 # Stored cost rows (every stride-th of steps 0..254) plus the header, rows of
 # E * 2 bytes; the header (16 bytes and 256 fp16 inputs) takes one row, two at
 # K = 8 where a row is 512 bytes.
-@pytest.mark.parametrize("k,per_tile", [(1, 33 * 65536), (2, 52 * 32768), (3, 129 * 16384),
+@pytest.mark.parametrize("k,per_tile", [(1, 33 * 65536), (2, 52 * 32768), (3, 86 * 16384),
                                         (4, 129 * 8192), (5, 256 * 4096), (6, 256 * 2048),
                                         (7, 256 * 1024), (8, 257 * 512)])
 def test_layout_formula(k, per_tile):
@@ -57,7 +57,7 @@ def test_estimator_validation_and_max_batch():
     assert max_b == (288 * 10 ** 9 - 8 * BYTES_PER_GIB) // (52 * 32768 + 2 * 16384 * 2)
     max_b, _ = ScratchEstimator.calculate_max_batch_size(
         k=3, available_vram_bytes=64 * BYTES_PER_GIB, max_single_alloc_bytes=16 * BYTES_PER_MIB)
-    assert max_b == 16 * BYTES_PER_MIB // (129 * 16384)
+    assert max_b == 16 * BYTES_PER_MIB // (86 * 16384)
     with pytest.raises(ValueError):
         ScratchEstimator.calculate_max_batch_size(k=2, available_vram_bytes=BYTES_PER_GIB)
 

@@ -86,7 +86,7 @@ def _predecessors(edges, K):
     return ((k[None, :] << (16 - K)) | np.asarray(edges)[:, None]).reshape(-1) >> K
 
 
-@pytest.mark.parametrize("K,stride,run", [(2, 5, 1024), (3, 2, 16), (4, 2, 64)])
+@pytest.mark.parametrize("K,stride,run", [(2, 5, 1024), (3, 3, 512), (4, 2, 64)])
 def test_cost_rows_keep_traceback_trees_together(K, stride, run):
     """A stored row serves `stride` steps; the traceback reads, per stored
     row, the 2^(K stride) costs `stride` predecessor steps below one edge.
