@@ -202,6 +202,72 @@ def test_fused_ldlq_steps_match_host_traversal(torch_mod, shapes):
         assert g.encoder_calls == c.encoder_calls
 
 
+def _ldlq_call(torch, widths, seed):
+    """Device matrices of one LDLQ encoder call over blocks of the given
+    widths (16 rows each) and its exl3_ldlq_block table."""
+    from exl3_intel_arc_quantizer_amd import _native
+    rng = np.random.default_rng(seed)
+    blocks, rows, tile0 = [], [], 0
+    for n in widths:
+        W = torch.from_numpy(rng.standard_normal((16, n)).astype(np.float32) * 3).cuda()
+        C = torch.from_numpy(rng.standard_normal((16, n)).astype(np.float32)).cuda()
+        Wq = torch.full((16, n), 7.0, device="cuda")
+        E = torch.full((16, n), 7.0, device="cuda")
+        S = torch.zeros((n // 16, 256), dtype=torch.int16, device="cuda")
+        blocks.append((W, C, Wq, E, S))
+        rows.append([W.data_ptr(), C.data_ptr(), Wq.data_ptr(), E.data_ptr(), S.data_ptr(), n,
+                     tile0, 0])
+        tile0 += n // 16
+    _native.check_ldlq_rows(rows, tile0)
+    table = torch.tensor(rows, dtype=torch.int64, device="cuda")
+    return blocks, table, tile0
+
+
+def _tiles_of(torch, m, perm):
+    """(n / 16, 256) tiles of a 16 x n matrix in tensor-core order: element p
+    of tile t is m[perm[p] // 16][16 t + perm[p] % 16]."""
+    n = m.shape[1]
+    t = m.reshape(16, n // 16, 16).permute(1, 0, 2).reshape(n // 16, 256)
+    return t[:, torch.from_numpy(perm).to(m.device)]
+
+
+@pytest.mark.parametrize("widths", [[16 * 5], [16 * 3, 16 * 21, 16 * 9], [16 * 8, 16 * 16]])
+def test_ldlq_gather_and_scatter_kernels(torch_mod, widths):
+    """exl3_ldlq_gather against the tensor-core tiles of W + compensation
+    (NaN and inf - inf sums included), and exl3_ldlq_scatter's Wq, E and
+    states at the same places, for calls of one block and of several blocks
+    of different widths."""
+    torch = torch_mod
+    from exl3_intel_arc_quantizer_amd import _native
+    from oracle import trellis_format_ref
+    perm = trellis_format_ref.tensor_core_perm()
+    blocks, table, tiles = _ldlq_call(torch, widths, sum(widths))
+    W0, C0 = blocks[0][0], blocks[0][1]
+    W0[3, 5] = float("nan")
+    W0[15, widths[0] - 1] = float("inf")
+    C0[15, widths[0] - 1] = float("-inf")
+    want = torch.cat([_tiles_of(torch, W + C, perm) for W, C, *_ in blocks])
+    x = torch.full((tiles, 256), -5.0, device="cuda")
+    _native.ldlq_gather(table, x)
+    assert torch.equal(x.isnan(), want.isnan()) and int(x.isnan().sum()) == 2
+    assert torch.equal(torch.nan_to_num(x), torch.nan_to_num(want))
+
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    recon = torch.randn((tiles, 256), generator=gen).half().float().cuda()
+    idx = torch.randint(-32768, 32767, (tiles, 256), generator=gen, dtype=torch.int16).cuda()
+    _native.ldlq_scatter(table, recon, idx)
+    t0 = 0
+    for W, C, Wq, E, S in blocks:
+        nt = W.shape[1] // 16
+        assert torch.equal(_tiles_of(torch, Wq, perm), recon[t0:t0 + nt])
+        diff = _tiles_of(torch, W, perm) - recon[t0:t0 + nt]
+        got = _tiles_of(torch, E, perm)
+        assert torch.equal(got.isnan(), diff.isnan())
+        assert torch.equal(torch.nan_to_num(got), torch.nan_to_num(diff))
+        assert torch.equal(S, idx[t0:t0 + nt])
+        t0 += nt
+
+
 def test_hessian_from_half_activations_matches_float32(torch_mod):
     """calibration.py:337-385 on bf16 / fp16 activations: the half-precision
     GEMM with float32 output equals the float32 GEMM of the converted
