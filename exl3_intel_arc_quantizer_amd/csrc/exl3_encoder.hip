@@ -738,16 +738,21 @@ __global__ void __launch_bounds__(1024, 8) acs_forward_chunked(FwdArgs a) {
   const M map(tid);
 
   // cbv[jp][kk]: codebook values of branch kof(kk / 8, kk % 8) for the
-  // output pair (x(2 jp), x(2 jp + 1)).
+  // output pair (x(2 jp), x(2 jp + 1)). The state's three fields are
+  // disjoint bits and its hash is affine, so every hash is the group's hash
+  // plus the other fields times the multiplier: a few products per thread
+  // instead of a quarter-rate v_mul_lo_u32 per value.
+  const uint32_t HM = hash_mult(CB);
+  const uint32_t hh = hash_state(CB, (uint32_t)map.h << K);
   f16x2 cbv[JP][Q];
 #pragma unroll
   for (int jp = 0; jp < JP; ++jp)
 #pragma unroll
     for (int kk = 0; kk < Q; ++kk) {
-      const uint32_t s = ((uint32_t)map.kof(kk >> 3, kk & 7) << KR) | ((uint32_t)map.h << K);
+      const uint32_t hk = hh + ((uint32_t)map.kof(kk >> 3, kk & 7) << KR) * HM;
       f16x2 v;
-      v.x = decode_state(CB, s | (uint32_t)map.x(2 * jp));
-      v.y = decode_state(CB, s | (uint32_t)map.x(2 * jp + 1));
+      v.x = decode_hash(CB, hk + (uint32_t)map.x(2 * jp) * HM);
+      v.y = decode_hash(CB, hk + (uint32_t)map.x(2 * jp + 1) * HM);
       cbv[jp][kk] = v;
     }
   // Row gather: piece t (positions W t .. W t + W - 1 of the stored row) is
