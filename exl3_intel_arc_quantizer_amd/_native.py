@@ -592,17 +592,39 @@ def check_ldlq_rows(rows, tiles: int) -> None:
     for their addresses, so a table that breaks this is refused here."""
     import numpy as np
     r = np.asarray(rows, dtype=np.int64).reshape(-1, len(LDLQ_BLOCK_FIELDS))
-    if r.shape[0] < 1:
+    check_ldlq_table(r, [(0, r.shape[0], tiles)])
+
+
+def check_ldlq_table(rows, calls) -> None:
+    """``check_ldlq_rows`` for a whole traversal at once: ``rows`` holds the
+    ``exl3_ldlq_block`` rows of every call back to back and ``calls`` lists
+    each call's (first row, row count, tiles), in order and covering every
+    row."""
+    import numpy as np
+    r = np.asarray(rows, dtype=np.int64).reshape(-1, len(LDLQ_BLOCK_FIELDS))
+    c = np.asarray(calls, dtype=np.int64).reshape(-1, 3)
+    first, count, tiles = c[:, 0], c[:, 1], c[:, 2]
+    if (count < 1).any():
         raise ValueError("an LDLQ call needs at least one block")
+    if (not np.array_equal(first, np.concatenate([[0], np.cumsum(count)[:-1]]))
+            or int(count.sum()) != r.shape[0]):
+        raise ValueError("the calls must list the table's rows back to back")
     n = r[:, LDLQ_BLOCK_FIELDS.index("n")]
     tile0 = r[:, LDLQ_BLOCK_FIELDS.index("tile0")]
     if (n <= 0).any() or (n % 16).any():
         raise ValueError(f"block widths must be positive multiples of 16, got {n.tolist()}")
-    ends = np.cumsum(n // 16)
-    starts = np.concatenate([[0], ends[:-1]])
-    if not np.array_equal(tile0, starts) or int(ends[-1]) != int(tiles):
-        raise ValueError(f"blocks must tile the batch back to back from 0 to {tiles}: tile0 "
-                         f"{tile0.tolist()}, widths {(n // 16).tolist()}")
+    # Each row's start within its call: the widths of the call's earlier rows.
+    widths = n // 16
+    ends = np.cumsum(widths)
+    base = np.concatenate([[0], ends])[first]
+    starts = ends - widths - np.repeat(base, count)
+    call_bad = (np.add.reduceat((tile0 != starts).astype(np.int64), first) > 0) | (
+        ends[first + count - 1] - base != tiles)
+    if call_bad.any():
+        i = int(np.flatnonzero(call_bad)[0])
+        rows_i = slice(int(first[i]), int(first[i] + count[i]))
+        raise ValueError(f"blocks must tile the batch back to back from 0 to {int(tiles[i])}: "
+                         f"tile0 {tile0[rows_i].tolist()}, widths {widths[rows_i].tolist()}")
     for field in ("w", "comp", "wq", "err", "states"):
         if (r[:, LDLQ_BLOCK_FIELDS.index(field)] == 0).any():
             raise ValueError(f"NULL {field} address in an LDLQ block row")

@@ -227,14 +227,19 @@ class _Traversal:
         if r0 == i and i > 0:
             self.prod_cache[:i].addmm_(self.L[i:j, :i].T, self.err[i:j], alpha=1.0, beta=1.0)
 
-    def block_row(self, b: int, tile0: int) -> list:
-        """The ``exl3_ldlq_block`` fields of block b at batch tile ``tile0``."""
+    def block_row(self, b: int, tile0: int, bases: Optional[tuple] = None) -> list:
+        """The ``exl3_ldlq_block`` fields of block b at batch tile ``tile0``;
+        ``bases`` = ``block_bases()``, when the caller has it."""
         _, _, r0 = self.blocks[b]
         row = r0 * self.n * 4
-        return [self.weight.data_ptr() + row, self.prod_cache.data_ptr() + row,
-                self.weight_q.data_ptr() + row, self.err.data_ptr() + row,
-                self.encoded.data_ptr() + (r0 // 16) * self.tiles_n * 256 * 2,
-                self.n, tile0, 0]
+        w, comp, wq, err, states = bases if bases is not None else self.block_bases()
+        return [w + row, comp + row, wq + row, err + row,
+                states + (r0 // 16) * self.tiles_n * 256 * 2, self.n, tile0, 0]
+
+    def block_bases(self) -> tuple:
+        """Device addresses of W, the compensation rows, Wq, E and the states."""
+        return (self.weight.data_ptr(), self.prod_cache.data_ptr(), self.weight_q.data_ptr(),
+                self.err.data_ptr(), self.encoded.data_ptr())
 
     # ------------------------------------------------------- CPU steps
 
@@ -317,17 +322,21 @@ def _block_table(walks: List[_Traversal], steps: List[List[Tuple[int, int]]]):
         for t in (w.weight, w.prod_cache, w.weight_q, w.err, w.encoded):
             if not t.is_contiguous():
                 raise ValueError("LDLQ buffers must be contiguous")
-    from ._native import check_ldlq_rows
+    from ._native import check_ldlq_table
+    bases = [w.block_bases() for w in walks]
     rows, spans = [], []
     for call in steps:
         tile0 = 0
         first = len(rows)
         for w, b in call:
-            rows.append(walks[w].block_row(b, tile0))
+            rows.append(walks[w].block_row(b, tile0, bases[w]))
             tile0 += walks[w].tiles_n
-        check_ldlq_rows(rows[first:], tile0)
         spans.append((first, len(call), tile0))
-    table = torch.from_numpy(np.asarray(rows, dtype=np.int64)).to(walks[0].weight.device)
+    rows = np.asarray(rows, dtype=np.int64)
+    # One vectorised check for the whole traversal: call by call it took
+    # about 14 us of host time per call, all before the first call is queued.
+    check_ldlq_table(rows, spans)
+    table = torch.from_numpy(rows).to(walks[0].weight.device)
     return table, spans
 
 

@@ -126,3 +126,33 @@ def test_lanes_and_union_of_intervals():
     assert _lanes_of([walk(16, 8), walk(16, 32)]) == [[0, 1]]
     assert _union_seconds([(0.0, 1.0), (0.5, 2.0), (3.0, 4.0), (3.5, 3.6)]) == pytest.approx(3.0)
     assert _union_seconds([]) == 0.0
+
+
+def _block(n, tile0, w=1):
+    return [w, 2, 3, 4, 5, n, tile0, 0]
+
+
+def test_block_table_check_covers_every_call():
+    """check_ldlq_table (the host guard of the GPU traversal's block table,
+    one vectorised pass for every call) accepts back-to-back blocks and
+    names the first call that breaks a rule: a block start, a call's total,
+    a width, an empty or misplaced call, a NULL address; check_ldlq_rows is
+    the same check for one call."""
+    from exl3_intel_arc_quantizer_amd._native import check_ldlq_rows, check_ldlq_table
+    good = [_block(48, 0), _block(32, 3), _block(64, 0)]
+    check_ldlq_table(good, [(0, 2, 5), (2, 1, 4)])
+    check_ldlq_rows(good[:2], 5)
+    cases = [
+        ([_block(48, 0), _block(32, 2), _block(64, 0)], [(0, 2, 5), (2, 1, 4)], "0 to 5"),
+        (good, [(0, 2, 6), (2, 1, 4)], "0 to 6"),
+        ([_block(48, 0), _block(32, 3), _block(64, 1)], [(0, 2, 5), (2, 1, 4)], "0 to 4"),
+        ([_block(40, 0), _block(32, 3), _block(64, 0)], [(0, 2, 5), (2, 1, 4)], "multiples of 16"),
+        (good, [(0, 2, 5), (1, 1, 4)], "back to back"),
+        (good, [(0, 0, 0), (0, 2, 5), (2, 1, 4)], "at least one block"),
+        ([_block(48, 0), _block(32, 3), _block(64, 0, w=0)], [(0, 2, 5), (2, 1, 4)], "NULL w"),
+    ]
+    for rows, calls, msg in cases:
+        with pytest.raises(ValueError, match=msg):
+            check_ldlq_table(rows, calls)
+    with pytest.raises(ValueError, match="0 to 4"):
+        check_ldlq_rows(good[:2], 4)
